@@ -1,0 +1,133 @@
+/*
+ * sparse_attn.h -- C ABI of the gfx950 block-sparse attention library
+ * (libsparse_attn_hip.so).
+ *
+ * Plain pointers, sizes and element strides only: no torch or C++ types cross
+ * this boundary.  Every entry point returns 0 on success, a negative SA_E*
+ * code for a rejected argument, or a positive hipError_t from the runtime;
+ * sa_last_error() then describes the failure (thread-local, valid until the
+ * next call on the same thread).  Nothing here allocates device memory or
+ * synchronises: kernels are enqueued on the given stream (a hipStream_t,
+ * NULL = the default stream), and any scratch space is passed in by the
+ * caller.
+ *
+ * Tensor conventions (all strides in elements, innermost head dim contiguous):
+ *   q  [B, Hq,  T_q, D]      o [B, Hq, T_q, D]
+ *   k  [B, Hkv, T_k, D]      v [B, Hkv, T_k, D]      Hq % Hkv == 0
+ * Query head h reads KV head h / (Hq / Hkv), the head mapping of Hugging Face
+ * repeat_kv that the reference's Qwen3 integration applies before its kernel
+ * (sparse_llm/qwen3/integrations/modeling_sparse_qwen3.py:233-234).
+ *
+ * CSR schedule (sparse_attentions/patterns/base.py:26-33): for CSR row r and
+ * query block qb the retained key blocks are
+ *   pairs[r * pairs_stride + offsets[r * offsets_stride + qb] ...
+ *         pairs[r * pairs_stride + offsets[r * offsets_stride + qb + 1] - 1]
+ * There is one row per query head (csr_rows == Hq, the reference's layout) or
+ * one row per KV group shared by its Hq/Hkv query heads (csr_rows == Hkv).
+ */
+#ifndef SPARSE_ATTN_H
+#define SPARSE_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_ABI_VERSION 1
+
+/* element types */
+#define SA_DTYPE_BF16 0
+#define SA_DTYPE_F16 1
+
+/* argument error codes (negative) */
+#define SA_E_DTYPE (-1)      /* unsupported element type */
+#define SA_E_SHAPE (-2)      /* inconsistent or unsupported sizes */
+#define SA_E_HEADDIM (-3)    /* head dim not supported by the kernels */
+#define SA_E_BLOCK (-4)      /* unsupported block size */
+#define SA_E_CSR (-5)        /* csr_rows not Hq or Hkv */
+#define SA_E_NULL (-6)       /* required pointer is NULL */
+#define SA_E_WORKSPACE (-7)  /* workspace missing or too small */
+#define SA_E_ALIGN (-8)      /* pointer or stride breaks 16-byte vector access */
+
+/* Version of this ABI; a loader refuses a library whose value differs. */
+int sa_abi_version(void);
+
+/* Description of the last failure on the calling thread ("" if none). */
+const char* sa_last_error(void);
+
+/*
+ * Block-sparse causal attention over a CSR block schedule (prefill, and any
+ * T_q >= 1).  Replaces kernels/triton/universal_sparse_attn.py:165-238
+ * (universal_sparse_attn) and its kernel :45-160.
+ *
+ * Query row t sits at absolute position q_offset + t and sees key j iff the
+ * key block of j is retained for its query block, j <= q_offset + t and
+ * j < T_k.  q_offset = T_k - T_q reproduces the reference for T_q == T_k and
+ * T_q == 1 (universal_sparse_attn.py:203-205).  A row that sees no key is 0.
+ * Per row: out = sum_j softmax(q.k_j * sm_scale) v_j with fp32 accumulation;
+ * probabilities are rounded to the element type before the PV product, as in
+ * the reference kernel (:147).
+ *
+ * block_size: 64 or 128 (the CSR granularity; the kernel tiles by 64).
+ * head_dim D: 64 or 128.  nqb = number of CSR query blocks (offsets has
+ * nqb + 1 entries per row), nqb == ceil(T_q / block_size).
+ */
+int sa_prefill(int dtype,
+               const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+               const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+               void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+               const int32_t* pairs, int64_t pairs_stride,
+               const int32_t* offsets, int64_t offsets_stride,
+               int csr_rows, int nqb,
+               int B, int Hq, int Hkv, int T_q, int T_k, int D,
+               int block_size, int q_offset, float sm_scale,
+               void* stream);
+
+/*
+ * Sparse decode: one new query token per sequence against a KV cache, reading
+ * only the retained KV blocks.  Replaces the T_q == 1 use of the reference
+ * kernel (universal_sparse_attn.py:203-205 via triton_universal_backend.py:47-66)
+ * with a memory-bound kernel; adds a paged cache (the reference has none).
+ *
+ * q [B, Hq, D] (strides q_sb, q_sh); o likewise.
+ * KV addressing of (sequence b, KV head g, token t of logical block lb):
+ *   paged      (block_table != NULL): base + block_table[b*bt_stride + lb]*kv_sb
+ *                                      + g*kv_sh + (t % page)*kv_st
+ *   contiguous (block_table == NULL): base + b*kv_sb + g*kv_sh + t*kv_st
+ * where t = lb*page + i.  K and V share strides.  kv_lens[b] (or kv_len for
+ * every sequence when kv_lens == NULL) is the number of valid tokens.
+ *
+ * Retained blocks of (b, row): sel[b*sel_sb + row*sel_sr + i] for
+ * i in [sel_off[b*off_sb + row*off_sr], sel_off[b*off_sb + row*off_sr + 1]);
+ * sel_sb / off_sb may be 0 to share one schedule across the batch (the
+ * reference's CSR has no batch axis).  sel_rows is Hq or Hkv.
+ *
+ * page is the block size of both the cache pages and the schedule (16..128,
+ * a multiple of 16).  num_splits >= 1 splits each (b, row) list across
+ * workgroups; num_splits > 1 needs a workspace of
+ * sa_decode_workspace_bytes(B, Hq, D, num_splits) bytes (fp32 partials).
+ */
+int sa_decode(int dtype,
+              const void* q, int64_t q_sb, int64_t q_sh,
+              const void* k, const void* v,
+              int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+              const int32_t* block_table, int64_t bt_stride,
+              const int32_t* kv_lens, int kv_len,
+              const int32_t* sel, int64_t sel_sb, int64_t sel_sr,
+              const int32_t* sel_off, int64_t off_sb, int64_t off_sr,
+              int sel_rows,
+              void* o, int64_t o_sb, int64_t o_sh,
+              int B, int Hq, int Hkv, int D, int page, float sm_scale,
+              int num_splits, void* workspace, int64_t workspace_bytes,
+              void* stream);
+
+/* Bytes of fp32 workspace sa_decode needs for num_splits > 1 (0 otherwise). */
+int64_t sa_decode_workspace_bytes(int B, int Hq, int D, int num_splits);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSE_ATTN_H */

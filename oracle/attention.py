@@ -130,13 +130,15 @@ def _row_head_map(Hq: int, R: int) -> np.ndarray:
 
 def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pairs, offsets,
                            block_size: int, q_offset: int | None = None,
-                           compute_dtype=torch.float32, p_dtype=None) -> torch.Tensor:
+                           compute_dtype=torch.float32, p_dtype=None, rows=None) -> torch.Tensor:
     """Block-gather attention over a CSR schedule (fp32 by default), on q's device.
 
     ``q [B,Hq,T_q,D]``, ``k, v [B,Hkv,T_k,D]`` with ``Hq % Hkv == 0``;
     ``pairs/offsets`` have ``Hq`` rows or ``Hkv`` rows (one per KV group).
     ``q_offset`` defaults to ``T_k - T_q``.  ``p_dtype`` (e.g. bf16) rounds
-    the probabilities before the PV product, as the kernels do.  Returns fp32.
+    the probabilities before the PV product, as the kernels do.  ``rows``
+    (optional) lists the ``(head, query block)`` pairs to compute; the others
+    stay zero.  Returns fp32.
     """
     B, Hq, T_q, D = q.shape
     Hkv, T_k = k.shape[1], k.shape[2]
@@ -155,32 +157,32 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pa
     vf = v.to(compute_dtype)
     out = torch.zeros(B, Hq, T_q, D, dtype=torch.float32, device=dev)
     scale = 1.0 / math.sqrt(D)
-    for h in range(Hq):
+    todo = rows if rows is not None else [(h, qb) for h in range(Hq) for qb in range(nqb)]
+    for h, qb in todo:
         r = int(rowmap[h])
         kvh = h // n_rep
-        for qb in range(nqb):
-            q0, q1 = qb * bs, min(T_q, (qb + 1) * bs)
-            if q0 >= q1:
-                continue
-            kbs = pairs[r, offsets[r, qb]:offsets[r, qb + 1]].tolist()
-            if not kbs:
-                continue
-            kidx = torch.cat([torch.arange(kb * bs, min(T_k, (kb + 1) * bs)) for kb in kbs]).to(dev)
-            qs = qf[:, h, q0:q1]                        # [B, m, D]
-            ks = kf[:, kvh].index_select(1, kidx)       # [B, n, D]
-            vs = vf[:, kvh].index_select(1, kidx)
-            s = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * scale
-            q_abs = q_offset + torch.arange(q0, q1, device=dev)
-            allowed = kidx[None, :] <= q_abs[:, None]
-            s = s.masked_fill(~allowed[None], float("-inf"))
-            m = s.amax(dim=-1, keepdim=True)
-            m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
-            p = torch.exp(s - m)
-            l = p.sum(dim=-1, keepdim=True)
-            if p_dtype is not None:
-                p = p.to(p_dtype).to(compute_dtype)
-            o = torch.matmul(p, vs) / torch.where(l > 0, l, torch.ones_like(l))
-            out[:, h, q0:q1] = o.float()
+        q0, q1 = qb * bs, min(T_q, (qb + 1) * bs)
+        if q0 >= q1:
+            continue
+        kbs = pairs[r, offsets[r, qb]:offsets[r, qb + 1]].tolist()
+        if not kbs:
+            continue
+        kidx = torch.cat([torch.arange(kb * bs, min(T_k, (kb + 1) * bs)) for kb in kbs]).to(dev)
+        qs = qf[:, h, q0:q1]                        # [B, m, D]
+        ks = kf[:, kvh].index_select(1, kidx)       # [B, n, D]
+        vs = vf[:, kvh].index_select(1, kidx)
+        s = torch.matmul(qs, ks.transpose(1, 2).contiguous()) * scale
+        q_abs = q_offset + torch.arange(q0, q1, device=dev)
+        allowed = kidx[None, :] <= q_abs[:, None]
+        s = s.masked_fill(~allowed[None], float("-inf"))
+        m = s.amax(dim=-1, keepdim=True)
+        m = torch.where(torch.isfinite(m), m, torch.zeros_like(m))
+        p = torch.exp(s - m)
+        l = p.sum(dim=-1, keepdim=True)
+        if p_dtype is not None:
+            p = p.to(p_dtype).to(compute_dtype)
+        o = torch.matmul(p, vs) / torch.where(l > 0, l, torch.ones_like(l))
+        out[:, h, q0:q1] = o.float()
     return out
 
 

@@ -1,0 +1,86 @@
+"""``hip_block_sparse``: the gfx950 block-sparse backend.
+
+Drop-in for ``TritonUniversalBackend`` / ``TritonBigBirdBackend``
+(``sparse_attentions/attention/triton_universal_backend.py:24-103``,
+``triton_bigbird_backend.py:21-102``): same ``forward(q, k, v, pattern)``
+signature and ``actual_backend`` property, and it consumes the same
+``PatternMetadata`` fields (CSR ``block_pairs``/``block_pair_offsets``, or the
+padded ``kv_block_list``, plus ``block_size``).
+
+Differences from the reference, all deliberate:
+
+* No silent fallback.  Where the Triton backends quietly run the dense masked
+  path (CPU tensors, fp32, no block schedule), this backend raises, so a run
+  either executes the HIP kernels or fails loudly.
+* ``k``/``v`` may carry ``H_kv < H`` heads (grouped-query attention); the
+  caller need not ``repeat_kv``.  A CSR with ``H_kv`` rows is shared by the
+  query heads of each KV group, letting one K/V tile feed all of them.
+* ``kind == "dense"`` runs the kernels over a full causal schedule
+  (bottom-right aligned: the query is the last ``T_q`` positions).
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import ops
+from ..patterns.base import PatternMetadata, block_mask_to_csr, kv_block_list_to_pairs
+from .base import AttentionBackend
+
+_DENSE_BLOCK = 64
+
+
+class HipBlockSparseBackend(AttentionBackend):
+    """Block-sparse attention on hand-written HIP kernels for gfx950."""
+
+    def __init__(self):
+        self._last_actual_backend = "unknown"
+        self.last_kernel = None          # "prefill" or "decode" after a forward
+        self._dense_cache: dict = {}
+        self._list_cache: dict = {}
+
+    @property
+    def actual_backend(self) -> str:
+        return self._last_actual_backend
+
+    def _dense_schedule(self, T_q: int, T_k: int, rows: int, device) -> tuple:
+        key = (T_q, T_k, rows, str(device))
+        if key not in self._dense_cache:
+            bs = _DENSE_BLOCK
+            nqb, nkb = -(-T_q // bs), -(-T_k // bs)
+            qa = (T_k - T_q) // bs + torch.arange(nqb)
+            bm = (torch.arange(nkb)[None, :] <= qa[:, None])[None].expand(rows, nqb, nkb)
+            pairs, offsets = block_mask_to_csr(bm.contiguous())
+            self._dense_cache[key] = (pairs.to(device), offsets.to(device), bs)
+        return self._dense_cache[key]
+
+    def _list_schedule(self, kv_block_list: torch.Tensor) -> tuple:
+        key = (kv_block_list.data_ptr(), tuple(kv_block_list.shape), kv_block_list._version)
+        if key not in self._list_cache:
+            self._list_cache[key] = kv_block_list_to_pairs(kv_block_list)
+        return self._list_cache[key]
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                pattern: PatternMetadata) -> torch.Tensor:
+        if not q.is_cuda:
+            raise RuntimeError("hip_block_sparse runs on ROCm GPU tensors only; got a CPU tensor "
+                               "(this backend has no CPU fallback)")
+        if pattern.kind == "dense":
+            pairs, offsets, bs = self._dense_schedule(q.size(2), k.size(2), k.size(1), q.device)
+        elif pattern.kind in ("mask", "local"):
+            bs = pattern.block_size
+            if bs is None:
+                raise ValueError("hip_block_sparse needs a block-sparse schedule; pattern.block_size is None")
+            if pattern.block_pairs is not None and pattern.block_pair_offsets is not None:
+                pairs, offsets = pattern.block_pairs, pattern.block_pair_offsets
+            elif pattern.kv_block_list is not None:
+                pairs, offsets = self._list_schedule(pattern.kv_block_list)
+            else:
+                raise ValueError("hip_block_sparse needs block_pairs/block_pair_offsets or kv_block_list")
+        else:
+            raise NotImplementedError(
+                f"hip_block_sparse does not run pattern kind {pattern.kind!r} (data-dependent top-k "
+                "selection is not a block schedule)")
+        out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs)
+        self.last_kernel = "decode" if q.size(2) == 1 else "prefill"
+        self._last_actual_backend = "hip_block_sparse"
+        return out

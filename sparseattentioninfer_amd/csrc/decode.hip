@@ -1,0 +1,370 @@
+// Sparse decode: one query token per sequence over the retained KV blocks of a
+// (paged or contiguous) cache, gfx950.  Memory-bound: no MFMA.
+//
+// Semantics: the query is the newest token, so every cached key below kv_len of a
+// retained block is visible (the decode row of the causal mask,
+// sparse_attentions/attention/masked_sdpa.py:42-46; universal_sparse_attn.py:203-205);
+// softmax with fp32 statistics; a sequence/head with no visible key yields 0.
+//
+// Mapping:
+//  * one workgroup (4 waves) = (sequence b, schedule row r, split s): the NH query
+//    heads that read row r share every K/V load (GQA: one read per KV group);
+//  * a wave streams whole rounds of a retained block: each lane loads 16-byte
+//    chunks (8 head-dim elements) of K and V, D/8 consecutive lanes cover one key
+//    row, so a load instruction reads 64/(D/8) full rows back to back;
+//  * q.k partial dots are reduced across the D/8 lanes of a row with xor-shuffles;
+//    the online softmax keeps (m, l, acc) per head; waves merge through LDS, and
+//    splits (num_splits > 1) merge in decode_combine_kernel.
+#include "sa_common.h"
+
+namespace sa {
+
+struct DecodeArgs {
+  const elem_t* q;
+  int64_t q_sb, q_sh;
+  const elem_t* k;
+  const elem_t* v;
+  int64_t kv_sb, kv_sh, kv_st;
+  const int32_t* block_table;
+  int64_t bt_stride;
+  const int32_t* kv_lens;
+  int kv_len;
+  const int32_t* sel;
+  int64_t sel_sb, sel_sr;
+  const int32_t* sel_off;
+  int64_t off_sb, off_sr;
+  int rows, heads_per_row, head_splits;
+  elem_t* o;
+  int64_t o_sb, o_sh;
+  float* part;  // [splits][B][Hq][D + 2] when num_splits > 1
+  int B, Hq, Hkv, page, num_splits;
+  float scale_log2;
+};
+
+constexpr int DEC_WAVES = 4;
+constexpr int DEC_NI = 8;  // 16-byte loads of K (and of V) per lane per round
+
+template <bool BF16, int D, int NH>
+struct Decode {
+  using E = Elem<BF16>;
+  static constexpr int LPR = D / 8;        // lanes per key row
+  static constexpr int KPI = 64 / LPR;     // key rows per load instruction
+  static constexpr int CH = DEC_NI * KPI;  // keys per round
+
+  static __device__ __forceinline__ void unpack8(u32x4 w, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = E::to_f32(static_cast<elem_t>(w[i] & 0xffffu));
+      f[2 * i + 1] = E::to_f32(static_cast<elem_t>(w[i] >> 16));
+    }
+  }
+
+  static __device__ void run(const DecodeArgs& a) {
+    __shared__ float s_m[DEC_WAVES][NH];
+    __shared__ float s_l[DEC_WAVES][NH];
+    __shared__ float s_acc[DEC_WAVES][NH][D];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int dc = lane % LPR;  // head-dim chunk
+    const int kg = lane / LPR;  // key row within a load instruction
+
+    int wid = blockIdx.x;
+    const int s = wid % a.num_splits;
+    wid /= a.num_splits;
+    const int r = wid % a.rows;
+    wid /= a.rows;
+    const int hs = wid % a.head_splits;
+    const int b = wid / a.head_splits;
+    const int h0 = r * a.heads_per_row + hs * NH;  // first query head of this workgroup
+    const int kvh = h0 / (a.Hq / a.Hkv);
+
+    const int32_t* offp = a.sel_off + b * a.off_sb + r * a.off_sr;
+    const int lo_all = offp[0];
+    const int cnt = offp[1] - lo_all;
+    const int lo = lo_all + (int)((int64_t)cnt * s / a.num_splits);
+    const int hi = lo_all + (int)((int64_t)cnt * (s + 1) / a.num_splits);
+    const int32_t* selp = a.sel + b * a.sel_sb + r * a.sel_sr;
+    const int L = a.kv_lens ? a.kv_lens[b] : a.kv_len;
+    const int rpb = (a.page + CH - 1) / CH;  // rounds per block
+
+    float qv[NH][8];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      const u32x4 w = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + (h0 + h) * a.q_sh + dc * 8);
+      unpack8(w, qv[h]);
+    }
+
+    float m_run[NH], l_run[NH], acc[NH][8];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      m_run[h] = -__builtin_inff();
+      l_run[h] = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
+    }
+
+    const int n_items = (hi - lo) * rpb;
+    for (int it = wave; it < n_items; it += DEC_WAVES) {
+      const int lb = selp[lo + it / rpb];
+      const int k0 = (it % rpb) * CH;  // first key of the round in its block
+      // valid keys this round; blocks past kv_len (or negative ids) load nothing
+      const int nkeys = lb < 0 ? 0 : min(min(CH, a.page - k0), L - lb * a.page - k0);
+      if (nkeys <= 0) continue;
+      const elem_t* kb;
+      const elem_t* vb;
+      if (a.block_table) {
+        const int64_t pg = a.block_table[b * a.bt_stride + lb];
+        kb = a.k + pg * a.kv_sb + kvh * a.kv_sh + (int64_t)k0 * a.kv_st;
+        vb = a.v + pg * a.kv_sb + kvh * a.kv_sh + (int64_t)k0 * a.kv_st;
+      } else {
+        const int64_t t0 = (int64_t)lb * a.page + k0;
+        kb = a.k + b * a.kv_sb + kvh * a.kv_sh + t0 * a.kv_st;
+        vb = a.v + b * a.kv_sb + kvh * a.kv_sh + t0 * a.kv_st;
+      }
+      u32x4 kr[DEC_NI], vr[DEC_NI];
+#pragma unroll
+      for (int i = 0; i < DEC_NI; ++i) {
+        const int key = kg + KPI * i;
+        const bool ok = key < nkeys;
+        kr[i] = ok ? *reinterpret_cast<const u32x4*>(kb + key * a.kv_st + dc * 8) : u32x4{0, 0, 0, 0};
+        vr[i] = ok ? *reinterpret_cast<const u32x4*>(vb + key * a.kv_st + dc * 8) : u32x4{0, 0, 0, 0};
+      }
+      // scores: partial dot over this lane's 8 dims, reduced over the LPR lanes of a row
+      float sc[DEC_NI][NH];
+#pragma unroll
+      for (int i = 0; i < DEC_NI; ++i) {
+        float kf[8];
+        unpack8(kr[i], kf);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          float p = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) p = fmaf(qv[h][e], kf[e], p);
+          sc[i][h] = p;
+        }
+      }
+#pragma unroll
+      for (int msk = 1; msk < LPR; msk <<= 1)
+#pragma unroll
+        for (int i = 0; i < DEC_NI; ++i)
+#pragma unroll
+          for (int h = 0; h < NH; ++h) sc[i][h] += __shfl_xor(sc[i][h], msk, 64);
+
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int i = 0; i < DEC_NI; ++i) {
+          const float x = (kg + KPI * i < nkeys) ? sc[i][h] * a.scale_log2 : -__builtin_inff();
+          sc[i][h] = x;
+          mx = fmaxf(mx, x);
+        }
+#pragma unroll
+        for (int msk = LPR; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+        const float m_new = fmaxf(m_run[h], mx);
+        const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+        const float alpha = fast_exp2(m_run[h] - m_use);
+        m_run[h] = m_new;
+        l_run[h] *= alpha;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+#pragma unroll
+        for (int i = 0; i < DEC_NI; ++i) {
+          const float p = fast_exp2(sc[i][h] - m_use);
+          l_run[h] += p;
+          sc[i][h] = E::to_f32(E::from_f32(p));  // P rounded to the element type for PV
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < DEC_NI; ++i) {
+        float vf[8];
+        unpack8(vr[i], vf);
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(sc[i][h], vf[e], acc[h][e]);
+      }
+    }
+
+    // merge the key rows of the wave (lanes with equal dc), then the waves through LDS
+#pragma unroll
+    for (int msk = LPR; msk < 64; msk <<= 1)
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        l_run[h] += __shfl_xor(l_run[h], msk, 64);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], msk, 64);
+      }
+    // every lane of a row group holds the same sums; lanes 0..LPR-1 publish them
+    if (kg == 0) {
+#pragma unroll
+      for (int h = 0; h < NH; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_acc[wave][h][dc * 8 + e] = acc[h][e];
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        s_m[wave][h] = m_run[h];
+        s_l[wave][h] = l_run[h];  // lanes of one row group hold equal sums: each key counted once
+      }
+    }
+    __syncthreads();
+
+    for (int x = tid; x < NH * D; x += 64 * DEC_WAVES) {
+      const int h = x / D, d = x % D;
+      float M = -__builtin_inff();
+#pragma unroll
+      for (int w = 0; w < DEC_WAVES; ++w) M = fmaxf(M, s_m[w][h]);
+      const float Mu = M == -__builtin_inff() ? 0.f : M;
+      float Ls = 0.f, As = 0.f;
+#pragma unroll
+      for (int w = 0; w < DEC_WAVES; ++w) {
+        const float f = fast_exp2(s_m[w][h] - Mu);
+        Ls += s_l[w][h] * f;
+        As += s_acc[w][h][d] * f;
+      }
+      const int hq = h0 + h;
+      if (a.num_splits == 1) {
+        const float out = Ls > 0.f ? As / Ls : 0.f;
+        a.o[b * a.o_sb + hq * a.o_sh + d] = E::from_f32(out);
+      } else {
+        float* pp = a.part + (((int64_t)s * a.B + b) * a.Hq + hq) * (D + 2);
+        pp[d] = As;
+        if (d == 0) {
+          pp[D] = M;
+          pp[D + 1] = Ls;
+        }
+      }
+    }
+  }
+};
+
+template <bool BF16, int D, int NH>
+__global__ __launch_bounds__(64 * DEC_WAVES) void decode_kernel(DecodeArgs a) {
+  Decode<BF16, D, NH>::run(a);
+}
+
+// Merges split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+template <bool BF16>
+__global__ void decode_combine_kernel(const float* part, elem_t* o, int64_t o_sb, int64_t o_sh,
+                                      int B, int Hq, int D, int S) {
+  using E = Elem<BF16>;
+  const int bh = blockIdx.x;
+  const int b = bh / Hq, h = bh % Hq;
+  const int64_t stride_s = (int64_t)B * Hq * (D + 2);
+  const float* p0 = part + (int64_t)bh * (D + 2);
+  float M = -__builtin_inff();
+  for (int s = 0; s < S; ++s) M = fmaxf(M, p0[s * stride_s + D]);
+  const float Mu = M == -__builtin_inff() ? 0.f : M;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float Ls = 0.f, As = 0.f;
+    for (int s = 0; s < S; ++s) {
+      const float* ps = p0 + s * stride_s;
+      const float f = fast_exp2(ps[D] - Mu);
+      Ls += ps[D + 1] * f;
+      As += ps[d] * f;
+    }
+    o[b * o_sb + h * o_sh + d] = E::from_f32(Ls > 0.f ? As / Ls : 0.f);
+  }
+}
+
+template <bool BF16, int D>
+static hipError_t launch_decode_d(const DecodeArgs& a, int nh, int64_t grid, hipStream_t st) {
+  switch (nh) {
+    case 4: hipLaunchKernelGGL((decode_kernel<BF16, D, 4>), dim3(grid), dim3(64 * DEC_WAVES), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<BF16, D, 2>), dim3(grid), dim3(64 * DEC_WAVES), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<BF16, D, 1>), dim3(grid), dim3(64 * DEC_WAVES), 0, st, a); break;
+  }
+  return hipGetLastError();
+}
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace sa
+
+extern "C" int64_t sa_decode_workspace_bytes(int B, int Hq, int D, int num_splits) {
+  if (num_splits <= 1 || B <= 0 || Hq <= 0 || D <= 0) return 0;
+  return (int64_t)num_splits * B * Hq * (D + 2) * (int64_t)sizeof(float);
+}
+
+extern "C" int sa_decode(int dtype,
+                         const void* q, int64_t q_sb, int64_t q_sh,
+                         const void* k, const void* v,
+                         int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+                         const int32_t* block_table, int64_t bt_stride,
+                         const int32_t* kv_lens, int kv_len,
+                         const int32_t* sel, int64_t sel_sb, int64_t sel_sr,
+                         const int32_t* sel_off, int64_t off_sb, int64_t off_sr,
+                         int sel_rows,
+                         void* o, int64_t o_sb, int64_t o_sh,
+                         int B, int Hq, int Hkv, int D, int page, float sm_scale,
+                         int num_splits, void* workspace, int64_t workspace_bytes,
+                         void* stream) {
+  using namespace sa;
+  clear_error();
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F16)
+    return set_error(SA_E_DTYPE, "sa_decode: dtype %d is not bf16 (0) or f16 (1)", dtype);
+  if (B < 0 || Hq < 1 || Hkv < 1 || Hq % Hkv)
+    return set_error(SA_E_SHAPE, "sa_decode: bad heads Hq=%d Hkv=%d (B=%d)", Hq, Hkv, B);
+  if (D != 64 && D != 128)
+    return set_error(SA_E_HEADDIM, "sa_decode: head dim %d not supported (64, 128)", D);
+  if (page < 16 || page > 128 || page % 16)
+    return set_error(SA_E_BLOCK, "sa_decode: page/block size %d not supported (16..128, multiple of 16)", page);
+  if (sel_rows != Hq && sel_rows != Hkv)
+    return set_error(SA_E_CSR, "sa_decode: sel_rows=%d must be Hq=%d or Hkv=%d", sel_rows, Hq, Hkv);
+  if (num_splits < 1) return set_error(SA_E_SHAPE, "sa_decode: num_splits=%d < 1", num_splits);
+  if (B == 0) return 0;
+  if (!q || !k || !v || !o || !sel || !sel_off)
+    return set_error(SA_E_NULL, "sa_decode: NULL pointer argument");
+  if (!kv_lens && kv_len < 0) return set_error(SA_E_SHAPE, "sa_decode: kv_len=%d < 0", kv_len);
+  const int64_t strides[] = {q_sb, q_sh, kv_sb, kv_sh, kv_st};
+  for (int64_t s : strides)
+    if (s % 8) return set_error(SA_E_ALIGN, "sa_decode: stride %lld is not a multiple of 8 elements", (long long)s);
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v))
+    return set_error(SA_E_ALIGN, "sa_decode: q/k/v base pointers must be 16-byte aligned");
+  if (num_splits > 1 && (!workspace || workspace_bytes < sa_decode_workspace_bytes(B, Hq, D, num_splits)))
+    return set_error(SA_E_WORKSPACE, "sa_decode: num_splits=%d needs %lld workspace bytes", num_splits,
+                     (long long)sa_decode_workspace_bytes(B, Hq, D, num_splits));
+
+  DecodeArgs a;
+  a.q = static_cast<const elem_t*>(q);
+  a.q_sb = q_sb; a.q_sh = q_sh;
+  a.k = static_cast<const elem_t*>(k);
+  a.v = static_cast<const elem_t*>(v);
+  a.kv_sb = kv_sb; a.kv_sh = kv_sh; a.kv_st = kv_st;
+  a.block_table = block_table; a.bt_stride = bt_stride;
+  a.kv_lens = kv_lens; a.kv_len = kv_len;
+  a.sel = sel; a.sel_sb = sel_sb; a.sel_sr = sel_sr;
+  a.sel_off = sel_off; a.off_sb = off_sb; a.off_sr = off_sr;
+  a.rows = sel_rows;
+  a.heads_per_row = Hq / sel_rows;
+  const int nh = (a.heads_per_row % 4 == 0) ? 4 : (a.heads_per_row % 2 == 0) ? 2 : 1;
+  a.head_splits = a.heads_per_row / nh;
+  a.o = static_cast<elem_t*>(o);
+  a.o_sb = o_sb; a.o_sh = o_sh;
+  a.part = static_cast<float*>(workspace);
+  a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.page = page; a.num_splits = num_splits;
+  a.scale_log2 = sm_scale * 1.4426950408889634f;
+
+  const int64_t grid = (int64_t)num_splits * sel_rows * a.head_splits * B;
+  if (grid > 0x7fffffff) return set_error(SA_E_SHAPE, "sa_decode: grid too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool bf16 = dtype == SA_DTYPE_BF16;
+  hipError_t err;
+  if (D == 128)
+    err = bf16 ? launch_decode_d<true, 128>(a, nh, grid, st) : launch_decode_d<false, 128>(a, nh, grid, st);
+  else
+    err = bf16 ? launch_decode_d<true, 64>(a, nh, grid, st) : launch_decode_d<false, 64>(a, nh, grid, st);
+  if (err == hipSuccess && num_splits > 1) {
+    if (bf16)
+      hipLaunchKernelGGL(decode_combine_kernel<true>, dim3(B * Hq), dim3(D), 0, st, a.part, a.o, o_sb, o_sh, B, Hq, D, num_splits);
+    else
+      hipLaunchKernelGGL(decode_combine_kernel<false>, dim3(B * Hq), dim3(D), 0, st, a.part, a.o, o_sb, o_sh, B, Hq, D, num_splits);
+    err = hipGetLastError();
+  }
+  if (err != hipSuccess) return set_error((int)err, "sa_decode: launch failed: %s", hipGetErrorString(err));
+  return 0;
+}

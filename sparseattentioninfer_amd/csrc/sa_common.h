@@ -1,0 +1,69 @@
+// Shared device/host helpers for the gfx950 block-sparse attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/sparse_attn.h"
+
+namespace sa {
+
+// 16-bit element storage; the MFMA operand vectors reinterpret the same bits.
+typedef uint16_t elem_t;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Records a message for sa_last_error(); returns `code` for tail calls.
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+// Element-type traits: conversion to/from fp32 and the 32x32x16 MFMA.
+template <bool BF16>
+struct Elem;
+
+template <>
+struct Elem<true> {
+  static __device__ __forceinline__ float to_f32(elem_t x) {
+    return __uint_as_float(static_cast<uint32_t>(x) << 16);
+  }
+  // Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+  static __device__ __forceinline__ elem_t from_f32(float f) {
+    return __builtin_bit_cast(elem_t, static_cast<__bf16>(f));
+  }
+  static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Elem<false> {
+  static __device__ __forceinline__ float to_f32(elem_t x) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, x));
+  }
+  static __device__ __forceinline__ elem_t from_f32(float f) {
+    return __builtin_bit_cast(elem_t, static_cast<_Float16>(f));
+  }
+  static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// 2^x on the hardware transcendental unit (v_exp_f32); exp2(-inf) == 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value held by lane (lane ^ 32): the other half of a wave64.
+__device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
+
+__device__ __forceinline__ uint32_t pack2(elem_t lo, elem_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace sa

@@ -1,0 +1,187 @@
+"""Torch-facing operators over the gfx950 HIP library.
+
+``universal_sparse_attn`` and ``bigbird_sparse_attn`` keep the names, argument
+meaning and assertion messages of the reference's Triton entry points
+(``kernels/triton/universal_sparse_attn.py:165-238``,
+``kernels/triton/bigbird_sparse_attn.py:163-233``), so they are drop-ins.  Two
+extensions: ``k``/``v`` may carry fewer (KV) heads than ``q`` (grouped-query
+attention, query head ``h`` reads KV head ``h // (Hq / Hkv)``), and the CSR
+may hold one row per KV group.
+
+``paged_sparse_decode`` is new: one query token per sequence over a paged
+cache.  All work is enqueued on the current HIP stream; nothing synchronises.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from .patterns.base import kv_block_list_to_pairs
+
+_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    # The reference validates with `assert`; the same conditions raise AssertionError here,
+    # but independent of Python's -O flag.
+    if not cond:
+        raise AssertionError(msg)
+
+
+def _check_qkv(q, k, v, name):
+    _require(q.is_cuda, f"{name} requires CUDA tensors")
+    _require(k.is_cuda and v.is_cuda and k.device == q.device and v.device == q.device,
+             f"{name}: q, k and v must be on the same GPU")
+    _require(q.dtype in (torch.float16, torch.bfloat16), f"Expected fp16 or bf16, got {q.dtype}")
+    _require(k.dtype == q.dtype and v.dtype == q.dtype, f"{name}: q, k, v dtypes differ")
+    _require(q.dim() == 4 and k.dim() == 4 and v.dim() == 4, f"{name}: q, k, v must be [B, H, T, D]")
+    _require(k.shape == v.shape, f"{name}: k and v shapes differ")
+    _require(q.shape[0] == k.shape[0] and q.shape[3] == k.shape[3], f"{name}: batch/head-dim mismatch")
+    _require(q.shape[1] % k.shape[1] == 0,
+             f"{name}: {q.shape[1]} query heads not a multiple of {k.shape[1]} KV heads")
+    for t in (q, k, v):
+        _require(t.stride(3) == 1, f"{name}: the head dim must be contiguous")
+
+
+def universal_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                          block_pairs: torch.Tensor, block_pair_offsets: torch.Tensor,
+                          block_size: int, *, q_offset: int | None = None) -> torch.Tensor:
+    """Block-sparse causal attention over a CSR schedule; returns ``[B, Hq, T_q, D]``.
+
+    ``q [B, Hq, T_q, D]``, ``k, v [B, Hkv, T_k, D]`` fp16/bf16 on the GPU;
+    ``block_pairs [R, max_pairs]`` / ``block_pair_offsets [R, NQB+1]`` int32
+    with ``R == Hq`` or ``R == Hkv``.  Query row ``t`` is at absolute position
+    ``q_offset + t`` (default ``T_k - T_q``).  ``T_q == 1`` runs the decode
+    kernel (the reference runs its prefill kernel on one row).
+    """
+    name = "universal_sparse_attn"
+    _check_qkv(q, k, v, name)
+    B, Hq, T_q, D = q.shape
+    Hkv, T_k = k.shape[1], k.shape[2]
+    _require(block_size >= 16 and (block_size & (block_size - 1)) == 0,
+             "block_size must be a power of 2 and >= 16")
+    _require(block_pairs.dtype == torch.int32, "block_pairs must be int32")
+    _require(block_pair_offsets.dtype == torch.int32, "block_pair_offsets must be int32")
+    R = block_pairs.size(0)
+    _require(R in (Hq, Hkv), f"block_pairs head dim {R} != H={Hq} (or KV heads {Hkv})")
+    _require(block_pair_offsets.size(0) == R,
+             f"block_pair_offsets head dim {block_pair_offsets.size(0)} != H={R}")
+    _require(block_pairs.device == q.device and block_pair_offsets.device == q.device,
+             f"{name}: CSR tensors must be on the GPU of q")
+    pairs = block_pairs.contiguous()
+    offsets = block_pair_offsets.contiguous()
+    nqb = offsets.size(1) - 1
+    sm_scale = 1.0 / math.sqrt(D)
+    if q_offset is None:
+        q_offset = T_k - T_q
+    out = torch.empty(B, Hq, T_q, D, dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    if T_q == 1 and q_offset == T_k - 1:
+        _require(nqb == 1, f"{name}: decode expects one CSR query block, got {nqb}")
+        status = lib.sa_decode(
+            _DTYPES[q.dtype],
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k.data_ptr(), v.data_ptr(),
+            *_kv_strides(k, v, name),
+            None, 0, None, T_k,
+            pairs.data_ptr(), 0, pairs.stride(0),
+            offsets.data_ptr(), 0, offsets.stride(0),
+            R,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            B, Hq, Hkv, D, block_size, sm_scale,
+            1, None, 0, _stream(q))
+        _lib.check("sa_decode", status)
+        return out
+    _require(block_size in (64, 128), f"{name}: block_size {block_size} not supported by the "
+             "gfx950 prefill kernel (64, 128)")
+    status = lib.sa_prefill(
+        _DTYPES[q.dtype],
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        pairs.data_ptr(), pairs.stride(0),
+        offsets.data_ptr(), offsets.stride(0),
+        R, nqb, B, Hq, Hkv, T_q, T_k, D, block_size, int(q_offset), sm_scale, _stream(q))
+    _lib.check("sa_prefill", status)
+    return out
+
+
+def _kv_strides(k, v, name):
+    _require(k.stride() == v.stride(), f"{name}: k and v must share strides")
+    return k.stride(0), k.stride(1), k.stride(2)
+
+
+def bigbird_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                        kv_block_list: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Padded-list entry point (``bigbird_sparse_attn.py:163-233``): converts to CSR once."""
+    _check_qkv(q, k, v, "bigbird_sparse_attn")
+    pairs, offsets = kv_block_list_to_pairs(kv_block_list.to(q.device))
+    return universal_sparse_attn(q, k, v, pairs, offsets, block_size)
+
+
+def decode_workspace_bytes(B: int, Hq: int, D: int, num_splits: int) -> int:
+    return int(_lib.load().sa_decode_workspace_bytes(B, Hq, D, num_splits))
+
+
+def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
+                        block_table: torch.Tensor, kv_lens: torch.Tensor,
+                        sel: torch.Tensor, sel_off: torch.Tensor, *,
+                        num_splits: int = 1, workspace: torch.Tensor | None = None,
+                        out: torch.Tensor | None = None) -> torch.Tensor:
+    """One decode token per sequence over a paged cache, reading retained blocks only.
+
+    ``q [B, Hq, D]`` (or ``[B, Hq, 1, D]``); pools ``k_pages, v_pages
+    [P, Hkv, page, D]``; ``block_table [B, max_blocks]`` int32 (logical block
+    -> page); ``kv_lens [B]`` int32; ``sel [B, R, max_sel]`` / ``sel_off
+    [B, R, 2]`` int32 retained logical blocks per (sequence, row), R = Hq or
+    Hkv.  ``num_splits > 1`` splits each row over workgroups and needs a
+    byte workspace of :func:`decode_workspace_bytes` (allocated if omitted).
+    """
+    name = "paged_sparse_decode"
+    q3 = q.reshape(q.shape[0], q.shape[1], q.shape[-1]) if q.dim() == 4 else q
+    _require(q3.is_cuda and k_pages.is_cuda and v_pages.is_cuda, f"{name} requires GPU tensors")
+    _require(q3.dtype in _DTYPES and k_pages.dtype == q3.dtype and v_pages.dtype == q3.dtype,
+             f"{name}: q/k/v must share an fp16 or bf16 dtype")
+    _require(k_pages.shape == v_pages.shape and k_pages.dim() == 4, f"{name}: pools must be [P, Hkv, page, D]")
+    B, Hq, D = q3.shape
+    _, Hkv, page, Dk = k_pages.shape
+    _require(D == Dk and Hq % Hkv == 0, f"{name}: head mismatch")
+    for t in (block_table, kv_lens, sel, sel_off):
+        _require(t.dtype == torch.int32 and t.device == q3.device, f"{name}: index tensors must be int32 on the GPU")
+    _require(sel.dim() == 3 and sel_off.dim() == 3 and sel_off.shape[2] == 2, f"{name}: bad sel shapes")
+    R = sel.shape[1]
+    _require(R in (Hq, Hkv) and sel_off.shape[:2] == (B, R) and sel.shape[0] == B, f"{name}: bad sel rows")
+    _require(sel.stride(2) == 1 and block_table.stride(1) == 1 and kv_lens.is_contiguous()
+             and sel_off.stride(2) == 1, f"{name}: index tensors must be contiguous in the last dim")
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q3.dtype, device=q3.device)
+    lib = _lib.load()
+    if num_splits > 1:
+        need = decode_workspace_bytes(B, Hq, D, num_splits)
+        if workspace is None:
+            workspace = torch.empty(need, dtype=torch.uint8, device=q3.device)
+        _require(workspace.numel() * workspace.element_size() >= need, f"{name}: workspace too small")
+    status = lib.sa_decode(
+        _DTYPES[q3.dtype],
+        q3.data_ptr(), q3.stride(0), q3.stride(1),
+        k_pages.data_ptr(), v_pages.data_ptr(),
+        *_kv_strides(k_pages, v_pages, name),
+        block_table.data_ptr(), block_table.stride(0),
+        kv_lens.data_ptr(), 0,
+        sel.data_ptr(), sel.stride(0), sel.stride(1),
+        sel_off.data_ptr(), sel_off.stride(0), sel_off.stride(1),
+        R,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        B, Hq, Hkv, D, page, 1.0 / math.sqrt(D),
+        num_splits, workspace.data_ptr() if workspace is not None else None,
+        workspace.numel() * workspace.element_size() if workspace is not None else 0,
+        _stream(q3))
+    _lib.check("sa_decode", status)
+    return out.reshape(q.shape) if q.dim() == 4 else out

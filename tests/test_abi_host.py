@@ -1,0 +1,62 @@
+"""The C-ABI library loads on the CPU and exports every entry point the header declares."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from sparseattentioninfer_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _declared():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(sa_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.library_path().exists():
+        from sparseattentioninfer_amd import _build
+        _build.build(verbose=False)
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    assert {"sa_abi_version", "sa_last_error", "sa_prefill", "sa_decode",
+            "sa_decode_workspace_bytes"} <= _declared()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(str(_lib.library_path()))
+    for name in sorted(_declared()):
+        assert hasattr(raw, name), f"{name} declared in include/ but not exported"
+    assert set(_lib.SIGNATURES) == _declared()
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.sa_abi_version() == _lib.ABI_VERSION
+    assert isinstance(lib.sa_last_error(), bytes)
+
+
+def test_argument_errors_are_reported_without_a_gpu(lib):
+    # rejected before any HIP call: unsupported head dim
+    st = lib.sa_prefill(0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
+                        None, 0, None, 0, 4, 1, 1, 4, 4, 64, 64, 96, 64, 0, 0.1, None)
+    assert st == -3 and b"head dim 96" in lib.sa_last_error()
+    st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, None, 0, None, 0, 0, None, 0, 0,
+                       3, None, 0, 0, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
+    assert st == -5 and b"sel_rows=3" in lib.sa_last_error()
+    assert lib.sa_decode_workspace_bytes(2, 4, 128, 3) == 3 * 2 * 4 * 130 * 4
+    assert lib.sa_decode_workspace_bytes(2, 4, 128, 1) == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setenv("SPARSE_ATTN_HIP_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(_lib.HipLibraryError):
+        _lib.load()
