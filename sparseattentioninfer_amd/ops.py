@@ -185,3 +185,75 @@ def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.T
         _stream(q3))
     _lib.check("sa_decode", status)
     return out.reshape(q.shape) if q.dim() == 4 else out
+
+
+class PreparedLaunch:
+    """A validated kernel launch with bound pointers; ``__call__`` re-enqueues it.
+
+    The bound tensors are kept alive by this object.  Re-launching writes the
+    same output tensor; it enqueues on the stream that was current when the
+    launch was prepared.
+    """
+
+    def __init__(self, fn_name: str, args: list, keep: tuple, out: torch.Tensor):
+        self._fn = getattr(_lib.load(), fn_name)
+        self._name = fn_name
+        self._args = args
+        self._keep = keep
+        self.out = out
+
+    def __call__(self) -> torch.Tensor:
+        _lib.check(self._name, self._fn(*self._args))
+        return self.out
+
+
+def prepare_prefill(q, k, v, block_pairs, block_pair_offsets, block_size, *, out=None) -> PreparedLaunch:
+    """Validates like :func:`universal_sparse_attn` (T_q > 1) and binds the launch."""
+    name = "prepare_prefill"
+    _check_qkv(q, k, v, name)
+    B, Hq, T_q, D = q.shape
+    Hkv, T_k = k.shape[1], k.shape[2]
+    _require(T_q > 1 and block_size in (64, 128), f"{name}: needs T_q > 1 and block 64/128")
+    pairs = block_pairs.contiguous()
+    offsets = block_pair_offsets.contiguous()
+    _require(pairs.dtype == torch.int32 and offsets.dtype == torch.int32, f"{name}: CSR must be int32")
+    R = pairs.size(0)
+    _require(R in (Hq, Hkv) and offsets.size(0) == R, f"{name}: CSR rows {R} not Hq or Hkv")
+    if out is None:
+        out = torch.empty(B, Hq, T_q, D, dtype=q.dtype, device=q.device)
+    args = [
+        _DTYPES[q.dtype],
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
+        R, offsets.size(1) - 1, B, Hq, Hkv, T_q, T_k, D, block_size, T_k - T_q,
+        1.0 / math.sqrt(D), _stream(q)]
+    return PreparedLaunch("sa_prefill", args, (q, k, v, pairs, offsets), out)
+
+
+def prepare_paged_decode(q, k_pages, v_pages, block_table, kv_lens, sel, sel_off, *,
+                         num_splits: int = 1, out=None) -> PreparedLaunch:
+    """Validates like :func:`paged_sparse_decode` and binds the launch (workspace included)."""
+    q3 = q.reshape(q.shape[0], q.shape[1], q.shape[-1]) if q.dim() == 4 else q
+    B, Hq, D = q3.shape
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=q3.dtype, device=q3.device)
+    ws = None
+    if num_splits > 1:
+        ws = torch.empty(decode_workspace_bytes(B, Hq, D, num_splits), dtype=torch.uint8, device=q3.device)
+    paged_sparse_decode(q3, k_pages, v_pages, block_table, kv_lens, sel, sel_off,
+                        num_splits=num_splits, workspace=ws, out=out)   # validates once
+    Hkv, page = k_pages.shape[1], k_pages.shape[2]
+    args = [
+        _DTYPES[q3.dtype],
+        q3.data_ptr(), q3.stride(0), q3.stride(1),
+        k_pages.data_ptr(), v_pages.data_ptr(), k_pages.stride(0), k_pages.stride(1), k_pages.stride(2),
+        block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(), 0,
+        sel.data_ptr(), sel.stride(0), sel.stride(1), sel_off.data_ptr(), sel_off.stride(0), sel_off.stride(1),
+        sel.shape[1], out.data_ptr(), out.stride(0), out.stride(1),
+        B, Hq, Hkv, D, page, 1.0 / math.sqrt(D),
+        num_splits, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        _stream(q3)]
+    return PreparedLaunch("sa_decode", args, (q3, k_pages, v_pages, block_table, kv_lens, sel, sel_off, ws), out)

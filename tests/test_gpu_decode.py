@@ -63,9 +63,11 @@ def test_paged_decode_matches_oracle(case):
 
 
 def test_reference_bigbird_decode_through_backend():
-    """Reference-written decode CSR (block 16, one row per head) on a contiguous cache."""
-    case, d = golden_case("bb_dec_t2048_k64")
-    _say("[decode] reference bb_dec_t2048_k64")
+    """Reference-written decode CSR (keep-ratio groups, block 32, one row per head) on a
+    contiguous cache, against the reference's dense masked semantics on its own token mask.
+    (Block 32 is a layout where the reference's token mask and CSR describe the same pattern.)"""
+    case, d = golden_case("kr_groups_dec_t3000")
+    _say("[decode] reference kr_groups_dec_t3000")
     H, T_k = case["n_heads"], case["T_k"]
     q = seeded((2, H, 1, 128), 31, torch.bfloat16)
     k = seeded((2, H, T_k, 128), 32, torch.bfloat16)
@@ -77,7 +79,7 @@ def test_reference_bigbird_decode_through_backend():
     out = be.forward(q.to(DEV), k.to(DEV), v.to(DEV), meta)
     assert be.last_kernel == "decode"
     want = oa.masked_sdpa(q.float(), k.float(), v.float(), "mask", torch.from_numpy(d["mask"]))
-    assert_close_bf16(out, want, "bb_dec_t2048_k64")
+    assert_close_bf16(out, want, "kr_groups_dec_t3000")
 
 
 def test_config4_full_size_sampled():
