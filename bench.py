@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-sparse attention hot path on one MI355X.
+
+Primary line (``value``): effective TFLOP/s of the block-sparse prefill at the
+Qwen3-4B attention shape (configs[2]: B=1, 32 query / 8 KV heads, head dim
+128, 32768 tokens, block 64, BigBird window 3 / global 2 / seeded random
+counts (0,1,2,3,3,4,6,8) per KV group), counting retained blocks only
+(4 * 64 * 64 * 128 FLOP per retained (query head, query block, key block)).
+
+Also reported (``decode``): the paged sparse decode of configs[3] (B=64
+sequences, 16384 cached tokens each in 64-token pages, 14 retained blocks per
+(sequence, KV head)) in tokens/s and HBM GB/s; and ``cpu_baseline``: the
+dense-masked PyTorch path (the reference's ``MaskedSdpaBackend`` arithmetic,
+restated in ``oracle/``) on the host cores, on a bounded sample of configs[2].
+
+Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
+``--gpus`` above 1 is refused: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "effective sparse-attn TFLOP/s + decode tok/s, Qwen3-4B-shape BigBird bf16, 1 GPU"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+BS = 64
+PAIR_FLOP = 4 * BS * BS     # x head_dim
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=("all", "prefill", "decode"), default="all",
+                    help="restrict to one kernel (for profiler runs)")
+    ap.add_argument("--decode-splits", type=int, default=0, help="0 = time 1 and 2, keep the faster")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a 1 GiB device copy (for scaling FETCH_SIZE / WRITE_SIZE counters)")
+    return ap.parse_args()
+
+
+def _events_time(launch, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        launch()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        launch()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, e0.elapsed_time(e1) / 1e3
+
+
+def prefill_workload(dev):
+    """q, k scaled per head dim by s ~ U(0.5, 2); v ~ N(0, 1)."""
+    import torch
+    from sparseattentioninfer_amd.patterns import block_mask_to_csr, seeded_bigbird_block_mask
+    T, Hq, Hkv, D = 32768, 32, 8, 128
+    cpu = torch.Generator().manual_seed(2024)
+    dim_scale = torch.empty(D).uniform_(0.5, 2.0, generator=cpu).to(dev)
+    g = torch.Generator(device=dev).manual_seed(2025)
+    q = (torch.randn(1, Hq, T, D, generator=g, device=dev) * dim_scale).to(torch.bfloat16)
+    k = (torch.randn(1, Hkv, T, D, generator=g, device=dev) * dim_scale).to(torch.bfloat16)
+    v = torch.randn(1, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+    nqb = T // BS
+    bm = seeded_bigbird_block_mask(Hkv, nqb, nqb, window=3, global_blocks=2,
+                                   random_blocks=[0, 1, 2, 3, 3, 4, 6, 8], seed=7)
+    pairs, offsets = block_mask_to_csr(bm)
+    nnz_group = bm.sum(dim=(1, 2))
+    causal_blocks = nqb * (nqb + 1) // 2
+    info = {
+        "workload": "configs[2] BigBird block-sparse causal prefill, Qwen3-4B attention shape",
+        "batch": 1, "seq_len": T, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block": BS,
+        "pattern": "window 3 (trailing) + global 2 + seeded random (0,1,2,3,3,4,6,8) per KV group",
+        "csr_rows": "per KV group (shared by its 4 query heads)",
+        "retained_pairs": int(nnz_group.sum().item()) * (Hq // Hkv),
+        "group_density": [round(x / causal_blocks, 4) for x in nnz_group.tolist()],
+    }
+    flops = info["retained_pairs"] * PAIR_FLOP * D
+    return (q, k, v, pairs.to(dev), offsets.to(dev), bm), info, flops
+
+
+def run_prefill(args, dev):
+    import torch
+    from sparseattentioninfer_amd import ops
+    (q, k, v, pairs, offsets, bm), info, flops = prefill_workload(dev)
+    launch = ops.prepare_prefill(q, k, v, pairs, offsets, BS)
+    wall, ev = _events_time(launch, args.steps, args.warmup)
+    avg = ev / args.steps
+    res = {
+        "value": flops / (wall / args.steps) / 1e12,
+        "ms_per_step": wall / args.steps * 1e3,
+        "kernel_us": avg * 1e6,
+        "flops_per_launch": flops,
+        "info": info,
+        "roofline": {"bound": "mfma", "achieved": flops / avg / 1e12, "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None},
+        "tensors": (q, k, v, bm),
+    }
+    return res
+
+
+def decode_workload(dev):
+    """paged bf16 cache, 64 sequences x 16384 tokens, BigBird-style block selection."""
+    import torch
+    from sparseattentioninfer_amd.patterns import decode_selection
+    B, Hq, Hkv, D, page, L = 64, 32, 8, 128, 64, 16384
+    nblk = L // page
+    P = B * nblk
+    g = torch.Generator(device=dev).manual_seed(4048)
+    kp = torch.randn(P, Hkv, page, D, generator=g, device=dev).to(torch.bfloat16)
+    vp = torch.randn(P, Hkv, page, D, generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn(B, Hq, D, generator=g, device=dev).to(torch.bfloat16)
+    table = torch.randperm(P, generator=torch.Generator().manual_seed(4049)).to(torch.int32).reshape(B, nblk)
+    lens = torch.full((B,), L, dtype=torch.int32)
+    sel, sel_off = decode_selection(B, Hkv, nblk, local=4, global_blocks=2, random_blocks=8, seed=4050)
+    kept = int(sel_off[:, :, 1].sum().item())           # (sequence, KV head, block) triples
+    kv_bytes = kept * page * D * 2 * 2
+    io_bytes = 2 * B * Hq * D * 2                        # q in, o out
+    idx_bytes = (kept + sel_off.numel() + B) * 4 + kept * 4   # sel + offsets + lens + block-table reads
+    info = {"workload": "configs[3] paged sparse decode", "batch": B, "q_heads": Hq, "kv_heads": Hkv,
+            "head_dim": D, "kv_len": L, "page": page, "retained_blocks_per_row": kept // (B * Hkv),
+            "retained_fraction": round(kept / (B * Hkv * nblk), 4)}
+    t = [x.to(dev) for x in (q, kp, vp, table, lens, sel, sel_off)]
+    return t, info, kv_bytes + io_bytes + idx_bytes
+
+
+def run_decode(args, dev):
+    from sparseattentioninfer_amd import ops
+    (q, kp, vp, table, lens, sel, sel_off), info, nbytes = decode_workload(dev)
+    steps = max(10 * args.steps, 100)
+    best = None
+    for splits in ([args.decode_splits] if args.decode_splits else [1, 2]):
+        launch = ops.prepare_paged_decode(q, kp, vp, table, lens, sel, sel_off, num_splits=splits)
+        wall, ev = _events_time(launch, steps, max(args.warmup, 10))
+        cand = (ev / steps, wall / steps, splits)
+        if best is None or cand[0] < best[0]:
+            best = cand
+    avg, per_step, splits = best
+    gbs = nbytes / avg / 1e9
+    info["num_splits"] = splits
+    return {
+        **info,
+        "steps": steps,
+        "us_per_step": per_step * 1e6,
+        "kernel_us": avg * 1e6,
+        "tok_per_s": info["batch"] / per_step,
+        "bytes_per_launch": nbytes,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+    }
+
+
+def cpu_baseline(prefill_res, budget_s):
+    """Dense-masked fp32 attention (oracle restatement of masked_sdpa.py:23-68) on host cores,
+    over sampled (query head, query block) rows of configs[2]; effective TFLOP/s on the same
+    retained-block numerator as the GPU figure."""
+    import numpy as np
+    import torch
+    from oracle.attention import masked_sdpa_rows
+    q, k, v, bm = prefill_res["tensors"]
+    Hq, T, D = q.shape[1], q.shape[2], q.shape[3]
+    Hkv = k.shape[1]
+    n_rep = Hq // Hkv
+    kc = k[0].float().cpu()
+    vc = v[0].float().cpu()
+    rng = np.random.default_rng(0)
+    nqb = T // BS
+    flops = 0
+    n = 0
+    elapsed = 0.0
+    while elapsed < budget_s or n < 4:
+        h, qb = int(rng.integers(Hq)), int(rng.integers(nqb))
+        g = h // n_rep
+        qr = q[0, h, qb * BS:(qb + 1) * BS].float().cpu()
+        blk = bm[g, qb]                                              # [NKB] retained key blocks
+        keep = blk.repeat_interleave(BS)[None, :T].expand(BS, T)
+        keep = keep & (torch.arange(T)[None, :] <= (qb * BS + torch.arange(BS))[:, None])
+        t0 = time.perf_counter()
+        masked_sdpa_rows(qr, kc[g], vc[g], keep)
+        elapsed += time.perf_counter() - t0
+        flops += int(blk.sum().item()) * PAIR_FLOP * D
+        n += 1
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"{n} (query head, query block) rows of configs[2] drawn uniformly (seed 0); each row "
+                       f"dense-masked fp32 over all {T} keys as masked_sdpa.py does; {elapsed:.1f} s of CPU "
+                       f"time; host os.cpu_count()={os.cpu_count()}, affinity={aff}")}
+
+
+def copy_calibration(dev):
+    import torch
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "note": "3 device copies of 1 GiB; compare FETCH_SIZE/WRITE_SIZE"}))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are not part of "
+              "this build (see DESIGN.md: how the path would shard).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    if args.copy_calibration:
+        copy_calibration(dev)
+        return
+    line = {"metric": METRIC, "value": None, "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic: seeded N(0,1) q/k/v (q,k scaled per head dim by U(0.5,2)), seeded BigBird blocks"}
+    pre = None
+    if args.only in ("all", "prefill"):
+        pre = run_prefill(args, dev)
+        line["value"] = round(pre["value"], 3)
+        line["ms_per_step"] = round(pre["ms_per_step"], 4)
+        line["config"] = {**pre["info"], "kernel_us": round(pre["kernel_us"], 2),
+                          "flops_per_launch": pre["flops_per_launch"]}
+        line["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre["roofline"].items()}
+    if args.only in ("all", "decode"):
+        dec = run_decode(args, dev)
+        dec["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()}
+        line["decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in dec.items()}
+        if pre is None:
+            line.update(value=round(dec["tok_per_s"], 1), unit="tok/s", ms_per_step=round(dec["us_per_step"] / 1e3, 4),
+                        config={"workload": dec["workload"]}, roofline=line["decode"]["roofline"])
+    if pre is not None and not args.no_cpu_baseline:
+        cb = cpu_baseline(pre, args.cpu_seconds)
+        cb["value"] = round(cb["value"], 5)
+        line["cpu_baseline"] = cb
+    traffic = ROOT / "profiles" / "traffic.json"
+    if traffic.exists() and "roofline" in line:
+        try:
+            t = json.loads(traffic.read_text())
+            key = "prefill" if pre is not None else "decode"
+            if key in t:
+                line["roofline"]["traffic"] = t[key]["hbm_bytes_per_launch"]
+            if "decode" in line and "decode" in t:
+                line["decode"]["roofline"]["traffic"] = t["decode"]["hbm_bytes_per_launch"]
+        except (ValueError, KeyError):
+            pass
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

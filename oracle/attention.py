@@ -73,6 +73,21 @@ def masked_sdpa(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kind: str,
     return torch.matmul(attn, v)
 
 
+def masked_sdpa_rows(q_rows: torch.Tensor, k: torch.Tensor, v: torch.Tensor, keep_rows: torch.Tensor) -> torch.Tensor:
+    """:func:`masked_sdpa` for a chunk of query rows of one head: dense scores against
+    every key, ``-inf`` where ``keep_rows`` is False, softmax, NaN rows -> 0, times V.
+
+    ``q_rows [m, D]``, ``k, v [T_k, D]``, ``keep_rows [m, T_k]`` bool (the pattern
+    mask already ANDed with the causal mask).  Same arithmetic as
+    ``masked_sdpa.py:35-68`` restricted to those rows, so the dense-masked CPU
+    path can be timed on a bounded sample of a workload too large to materialise.
+    """
+    scores = torch.matmul(q_rows, k.transpose(0, 1).contiguous()) * (1.0 / math.sqrt(q_rows.shape[-1]))
+    scores = scores.masked_fill(~keep_rows, float("-inf"))
+    attn = torch.nan_to_num(F.softmax(scores, dim=-1), nan=0.0)
+    return torch.matmul(attn, v)
+
+
 def textbook_attention(q, k, v, keep) -> np.ndarray:
     """float64 loop definition: ``out[i] = sum_j softmax_j(q_i.k_j / sqrt(D))[keep] v_j``.
 

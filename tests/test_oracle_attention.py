@@ -133,3 +133,15 @@ def test_paged_decode_matches_block_sparse():
             offs[r, 1] = n
         want = oa.block_sparse_attention(q[b:b + 1, :, None], k, v, pairs, offs, page)
         torch.testing.assert_close(got[b], want[0, :, 0], atol=1e-5, rtol=0)
+
+
+def test_masked_sdpa_rows_equals_full_masked_sdpa():
+    """The row-chunk form used for the CPU baseline equals masked_sdpa on those rows."""
+    T, H = 24, 2
+    q, k, v = (_rand((1, H, T, 8), s) for s in (51, 52, 53))
+    mask = torch.from_numpy(np.random.default_rng(3).random((H, T, T)) < 0.4)
+    full = oa.masked_sdpa(q, k, v, "mask", mask)
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))
+    for h in range(H):
+        rows = oa.masked_sdpa_rows(q[0, h, 5:17], k[0, h], v[0, h], (mask[h] & causal)[5:17])
+        torch.testing.assert_close(rows, full[0, h, 5:17], atol=1e-12, rtol=0)
