@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 1
+#define SA_ABI_VERSION 2
 
 /* element types */
 #define SA_DTYPE_BF16 0
@@ -72,6 +72,13 @@ const char* sa_last_error(void);
  * block_size: 64 or 128 (the CSR granularity; the kernel tiles by 64).
  * head_dim D: 64 or 128.  nqb = number of CSR query blocks (offsets has
  * nqb + 1 entries per row), nqb == ceil(T_q / block_size).
+ *
+ * workspace (optional, sa_prefill_workspace_bytes() bytes, 4-byte aligned):
+ * with it the kernel runs one persistent workgroup per resident slot that
+ * claims work items from a counter pair in the workspace.  It must be zeroed
+ * before its first use; every completed launch leaves it zeroed again.
+ * Launches that may run concurrently must not share one workspace.  NULL
+ * launches one workgroup per work item instead.
  */
 int sa_prefill(int dtype,
                const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
@@ -83,7 +90,11 @@ int sa_prefill(int dtype,
                int csr_rows, int nqb,
                int B, int Hq, int Hkv, int T_q, int T_k, int D,
                int block_size, int q_offset, float sm_scale,
+               void* workspace, int64_t workspace_bytes,
                void* stream);
+
+/* Bytes of the optional sa_prefill workspace (a counter pair). */
+int64_t sa_prefill_workspace_bytes(void);
 
 /*
  * Sparse decode: one new query token per sequence against a KV cache, reading

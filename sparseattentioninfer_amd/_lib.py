@@ -11,7 +11,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 
@@ -35,8 +35,10 @@ SIGNATURES = {
         _i32, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i32, _i32, _f32,
+        _vp, _i64,
         _vp,
     ]),
+    "sa_prefill_workspace_bytes": (_i64, []),
     "sa_decode": (_i32, [
         _i32,
         _vp, _i64, _i64,

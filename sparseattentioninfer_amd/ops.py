@@ -27,6 +27,25 @@ def _stream(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
+_PREFILL_WS: dict = {}
+
+
+def _prefill_workspace(t: torch.Tensor) -> torch.Tensor:
+    """Zeroed counter pair for the persistent prefill kernel, one per (device, stream).
+
+    Each launch leaves it zeroed again; launches on one stream run in order, so
+    they can share it.
+    """
+    stream = _stream(t)
+    key = (t.device.index, stream)
+    ws = _PREFILL_WS.get(key)
+    if ws is None:
+        nbytes = int(_lib.load().sa_prefill_workspace_bytes())
+        ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=t.device)
+        _PREFILL_WS[key] = ws
+    return ws
+
+
 def _require(cond: bool, msg: str) -> None:
     # The reference validates with `assert`; the same conditions raise AssertionError here,
     # but independent of Python's -O flag.
@@ -108,9 +127,14 @@ def universal_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         pairs.data_ptr(), pairs.stride(0),
         offsets.data_ptr(), offsets.stride(0),
-        R, nqb, B, Hq, Hkv, T_q, T_k, D, block_size, int(q_offset), sm_scale, _stream(q))
+        R, nqb, B, Hq, Hkv, T_q, T_k, D, block_size, int(q_offset), sm_scale,
+        *_ws_args(_prefill_workspace(q)), _stream(q))
     _lib.check("sa_prefill", status)
     return out
+
+
+def _ws_args(ws: torch.Tensor):
+    return ws.data_ptr(), ws.numel() * ws.element_size()
 
 
 def _kv_strides(k, v, name):
@@ -229,7 +253,7 @@ def prepare_prefill(q, k, v, block_pairs, block_pair_offsets, block_size, *, out
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
         pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
         R, offsets.size(1) - 1, B, Hq, Hkv, T_q, T_k, D, block_size, T_k - T_q,
-        1.0 / math.sqrt(D), _stream(q)]
+        1.0 / math.sqrt(D), *_ws_args(_prefill_workspace(q)), _stream(q)]
     return PreparedLaunch("sa_prefill", args, (q, k, v, pairs, offsets), out)
 
 

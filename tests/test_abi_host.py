@@ -27,7 +27,7 @@ def lib():
 
 
 def test_header_declares_entry_points():
-    assert {"sa_abi_version", "sa_last_error", "sa_prefill", "sa_decode",
+    assert {"sa_abi_version", "sa_last_error", "sa_prefill", "sa_prefill_workspace_bytes", "sa_decode",
             "sa_decode_workspace_bytes"} <= _declared()
 
 
@@ -46,13 +46,14 @@ def test_abi_version_and_error_string(lib):
 def test_argument_errors_are_reported_without_a_gpu(lib):
     # rejected before any HIP call: unsupported head dim
     st = lib.sa_prefill(0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
-                        None, 0, None, 0, 4, 1, 1, 4, 4, 64, 64, 96, 64, 0, 0.1, None)
+                        None, 0, None, 0, 4, 1, 1, 4, 4, 64, 64, 96, 64, 0, 0.1, None, 0, None)
     assert st == -3 and b"head dim 96" in lib.sa_last_error()
     st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, None, 0, None, 0, 0, None, 0, 0,
                        3, None, 0, 0, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
     assert st == -5 and b"sel_rows=3" in lib.sa_last_error()
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 3) == 3 * 2 * 4 * 130 * 4
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 1) == 0
+    assert lib.sa_prefill_workspace_bytes() == 8
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -151,3 +151,33 @@ def test_config3_full_size_sampled_rows():
     ref = torch.stack([want[0, h, qb * bs:(qb + 1) * bs] for h, qb in rows])
     assert_close_bf16(got, ref, "config3 sampled")
     assert torch.isfinite(out.float()).all()
+
+
+def test_persistent_and_grid_launches_agree_and_reset_workspace():
+    """The counter-driven persistent launch and the one-workgroup-per-item launch give identical
+    bits, and every persistent launch leaves its workspace zeroed."""
+    _say("[prefill] persistent vs grid launch")
+    from sparseattentioninfer_amd import _lib
+    B, Hq, Hkv, T, D, bs = 2, 8, 2, 777, 128, 64
+    bm = bernoulli_block_mask(Hkv, -(-T // bs), -(-T // bs), density=0.3, seed=4)
+    pairs, offsets = (x.to(DEV) for x in block_mask_to_csr(bm))
+    q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=12))
+    lib = _lib.load()
+    ws = torch.zeros(2, dtype=torch.int32, device=DEV)
+    outs = []
+    for w in (ws, None, ws, ws):
+        o = torch.empty_like(q)
+        st = lib.sa_prefill(0, q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
+                            v.data_ptr(), *v.stride()[:3], o.data_ptr(), *o.stride()[:3],
+                            pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
+                            Hkv, offsets.size(1) - 1, B, Hq, Hkv, T, T, D, bs, 0, 1.0 / math.sqrt(D),
+                            w.data_ptr() if w is not None else None, 8 if w is not None else 0,
+                            torch.cuda.current_stream().cuda_stream)
+        assert st == 0, lib.sa_last_error()
+        torch.cuda.synchronize()
+        assert ws.tolist() == [0, 0]
+        outs.append(o)
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    want = oa.block_sparse_attention(q, k, v, pairs.cpu(), offsets.cpu(), bs)
+    assert_close_bf16(outs[0], want, "persistent")
