@@ -6,26 +6,28 @@
 // type before the PV product, output acc / (l > 0 ? l : 1).
 //
 // Mapping onto the hardware:
-//  * one workgroup = (batch b, CSR row r, 32-row query tile qt); one wave per query head
-//    that shares row r (GQA: the Hq/Hkv heads of a KV group share every K/V tile staged
-//    in LDS, so K/V are read once per group instead of once per head);
-//  * at most 256 registers per wave and ~75 KiB of LDS per workgroup, so two workgroups
-//    share a CU: one's load latency (Q, the first K/V tile, the CSR row) and epilogue
-//    overlap the other's compute, and two waves per SIMD let one wave's softmax (VALU)
-//    run under the other's matrix instructions;
+//  * one work item = (batch b, CSR row r, 64-row query tile qt, head split hs); its
+//    workgroup has two waves (two 32-row halves) per query head that shares row r, so the
+//    Hq/Hkv heads of a KV group share every K/V tile staged in LDS (GQA: K/V are read
+//    once per group, not once per head);
 //  * per wave and 64-key tile: S^T = K Q^T and O^T = V^T P^T on v_mfma_f32_32x32x16.
 //    Computing the transposed products puts one query row in each lane column, so the
 //    softmax statistics, the rescale of O and the P operand of the second product all
 //    stay in the lane that owns the row;
-//  * K rows are staged in LDS in a permuted order (krow) that makes each lane half of the
-//    S^T accumulator hold 8 consecutive keys per 16-key chunk; V is staged transposed
-//    ([d][key]), so the A operand of O^T = V^T P^T is one 16-byte LDS read per lane; the
-//    staging writes and the fragment reads of both layouts are bank-conflict free;
-//  * K/V tiles are double-buffered in LDS: the next tile is fetched into registers while
-//    the current one is computed, with one barrier per tile;
+//  * K/V tiles go from global memory straight into LDS (global_load_lds, no registers)
+//    in a swizzled layout whose fragment reads are bank-conflict free; the V^T operand is
+//    read with the transposing ds_read_b64_tr_b16, so V is staged row-major as loaded;
+//  * four-head workgroups (8 waves, one per SIMD pair) run a software pipeline: the next
+//    tile's S^T = K Q^T is issued under the current tile's exponentials, and its row max
+//    under the current tile's O^T += V^T P^T; Q is staged in LDS there to leave the
+//    registers to the accumulators.  Smaller workgroups run one tile at a time;
 //  * the softmax works in base 2 with scale*log2(e) folded into one FMA before the
 //    hardware v_exp_f32 (2^x); the row reference max is only raised (and O rescaled) when
-//    a row max exceeds it by more than 2^8, so the common case never touches O with VALU.
+//    a row max exceeds it by more than 2^8, so the common case never touches O with VALU;
+//  * O is written back through LDS so that every global store is a 16-byte piece of a
+//    contiguous row;
+//  * with a workspace, one persistent workgroup per CU slot claims work items from an
+//    atomic counter, heaviest query tiles first.
 //
 // MFMA 32x32x16 lane layouts used (l = lane, g = l / 32):
 //   A (32 x 16): lane l holds row l % 32, k = 8g .. 8g+7
@@ -45,6 +47,8 @@ constexpr int KT = 64;           // keys per K/V tile
 constexpr int ROW_CACHE = 1024;  // CSR entries of one row cached in LDS
 constexpr int N_XCD = 8;         // XCDs of an MI355X; workgroups are dealt to them in turn
 constexpr int XCD_CHUNK = 4;     // query tiles per chunk dealt to one XCD
+// Largest token stride (elements) of K and V: per-lane offsets within a tile are 32-bit.
+constexpr int64_t MAX_KV_STRIDE = (int64_t)1 << 24;
 
 struct PrefillArgs {
   const elem_t* q;
@@ -61,7 +65,7 @@ struct PrefillArgs {
   int64_t offsets_stride;
   int R;             // CSR rows
   int heads_per_row; // query heads that read one CSR row
-  int head_splits;   // heads_per_row / waves per workgroup
+  int head_splits;   // heads_per_row / heads per workgroup
   int B, Hq, Hkv, Tq, Tk;
   int ntq;           // 64-row query tiles
   int qpb_log2;      // log2(block_size / 64): query tiles per CSR block
@@ -71,85 +75,288 @@ struct PrefillArgs {
   unsigned int* counter;  // persistent mode: 2 zeroed counters (next item, finished workgroups)
 };
 
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(const void* p) {
+  return (__attribute__((address_space(3))) void*)(p);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)lds_ptr(p);
+}
+
+// Direct global -> LDS loads of 16 bytes per lane (global_load_lds_dwordx4: lane l's bytes
+// land at the LDS address in M0 plus 16 l).  They are issued from assembly so that the
+// compiler does not make every later LDS read wait for them (it cannot tell the staging
+// buffers apart); callers wait with wait_dma() before the barrier that publishes the data.
+// M0 is written one instruction ahead of its use by the load, as the hardware requires.
+//
+// Uniform base address `sbase` plus a per-lane 32-bit byte offset.
+__device__ __forceinline__ void load_lds16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory", "m0");
+}
+
+// Per-lane 64-bit address.
+__device__ __forceinline__ void load_lds16(const void* vaddr, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(vaddr), "s"(lds)
+      : "memory", "m0");
+}
+
+// Waits for the calling wave's direct loads (and any other vector memory access).
+__device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
 template <bool BF16, int D, int HW>
 struct Prefill {
   using E = Elem<BF16>;
-  static constexpr int NW = 2 * HW;         // waves: HW query heads x two 32-row halves
-  static constexpr int NT = 64 * NW;        // threads
-  static constexpr int KS = D + 8;          // sK row stride (elements), 16 B pad
-  static constexpr int VS = KT + 8;         // sVt row stride (elements), 16 B pad
-  static constexpr int DC = D / 8;          // 16-byte chunks per row
-  static constexpr int K_TOTAL = KT * DC;        // 16-byte K chunks per tile
-  static constexpr int V_TOTAL = DC * (KT / 4);  // V units (4 keys x 8 d) per tile
-  static constexpr int KCH = (K_TOTAL + NT - 1) / NT;
-  static constexpr int VUN = (V_TOTAL + NT - 1) / NT;
-  // Double-buffer and prefetch the next tile into registers during compute when that costs
-  // at most 32 VGPRs; one-wave workgroups single-buffer and stage after compute.
-  static constexpr bool PREFETCH = (KCH + 4 * VUN) <= 8;
-  static constexpr int NBUF = PREFETCH ? 2 : 1;
+  static constexpr int NW = 2 * HW;              // waves: HW query heads x two 32-row halves
+  static constexpr int NT = 64 * NW;             // threads
+  static constexpr int NCG = D / 32;             // column groups of a staged tile
+  static constexpr int TILE_BYTES = KT * D * 2;  // one staged K or V tile
+  static constexpr int NI = TILE_BYTES / 1024;   // 1 KiB wave-wide direct loads per tile
+  static constexpr int NIW = NI / NW;            // ... issued by each wave
+  static constexpr int WAVE_BYTES = QT * D * 2;  // 32 rows of Q or O (one wave's share)
+  // Four-head workgroups run the software-pipelined loop with K triple- and V double-
+  // buffered and Q staged in LDS.  Other shapes run one tile at a time over double-buffered
+  // K/V (single-buffered for one-head workgroups, so that more of them share a CU).
+  static constexpr bool PIPE = HW == 4;
+  static constexpr int NBK = PIPE ? 3 : (HW == 1 ? 1 : 2);
+  static constexpr int NBV = PIPE ? 2 : NBK;
+  static constexpr int LDS_KV = (NBK + NBV) * TILE_BYTES;
+  static constexpr int LDS_Q = PIPE ? NW * WAVE_BYTES : 16;
   static constexpr float RESCALE_LOG2 = 8.f;
+  static_assert(NI % NW == 0, "direct loads must split evenly over the waves");
+  static_assert(NW * WAVE_BYTES <= LDS_KV, "the epilogue stages O in the K/V buffers");
 
-  // LDS row of key k within a tile: bits 2 and 3 swapped.  With this order the S^T
-  // accumulator gives each lane half 8 consecutive keys per 16-key chunk, so the matching
-  // V^T operand is one contiguous 16-byte LDS read.
+  // LDS row of key k within a staged K tile: bits 2 and 3 swapped.  With this order the S^T
+  // accumulator gives each lane half 8 consecutive keys per 16-key chunk, the k-order of the
+  // V^T operand.
   static __device__ __forceinline__ int krow(int k) {
     return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1);
   }
 
-  struct Stage {
-    u32x4 kr[KCH];
-    u32x4 vr[VUN][4];
+  // ---- staging ------------------------------------------------------------------------
+  // Staged tile layout (K and V alike, 64 rows x D, no padding): D/32 column groups of
+  // 4 KiB; row r of a group is 64 bytes at r*64 holding 16-byte chunks c = 0..3 (columns
+  // 8c..8c+7 of the group) at position c ^ ((r >> 2) & 3).  One wave-wide direct load
+  // (global_load_lds, 16 bytes per lane, lane l at base + 16 l) fills 16 rows of one group;
+  // the K fragment reads (16 lanes: 16 consecutive rows, one chunk) and the transposing
+  // V^T reads (32 lanes: 4 rows x 64 bytes) are both bank-conflict free.
+  //
+  // Wave w issues the direct loads k = w*NIW .. w*NIW + NIW - 1 of a tile; load k fills
+  // column group k % NCG, rows 16 (k / NCG) .. + 15, and its lane l carries row
+  // 16 (k / NCG) + l/4, columns 32 (k % NCG) + col(l), col(l) = 8 ((l & 3) ^ ((l >> 4) & 3))
+  // ((row >> 2) & 3 == (l >> 4) & 3).  Either a wave's loads share one row block
+  // (NIW <= NCG) or they cover whole row blocks (NIW > NCG), so every per-load address
+  // difference is a compile-time constant or one uniform multiple of the row stride.
+  static_assert(NCG % NIW == 0 || NIW % NCG == 0, "direct loads must tile row blocks evenly");
+  static __device__ __forceinline__ int dma_col(int lane) { return 8 * ((lane & 3) ^ ((lane >> 4) & 3)); }
+
+  // Byte offset of this lane's 16 bytes within a direct load of K (rows permuted by krow)
+  // and of V, relative to the load's first row and column group; krow(16 rb + x) ==
+  // 16 rb + krow(x), so the rest of each load's address is uniform.
+  struct DmaLane {
+    uint32_t k, v;
+    __device__ __forceinline__ DmaLane(const PrefillArgs& a, int lane) {
+      k = (uint32_t)((krow(lane >> 2) * a.k_st + dma_col(lane)) * 2);
+      v = (uint32_t)(((lane >> 2) * a.v_st + dma_col(lane)) * 2);
+    }
   };
 
+  // Fills one staged tile of key tile kt from `base` (token stride st; lane offset off).
   // Rows past T_k read row T_k - 1: their scores are masked and their probabilities are 0.
-  static __device__ __forceinline__ void load(Stage& st, const elem_t* kb, const elem_t* vb,
-                                              const PrefillArgs& a, int kt, int tid) {
+  template <bool PERMUTE>
+  static __device__ __forceinline__ void dma(const elem_t* base, int64_t st, uint32_t off, char* tile, int kt,
+                                             int Tk, int wave, int lane) {
+    const char* tb = reinterpret_cast<const char*>(base + (int64_t)kt * KT * st);
+    const int k0 = wave * NIW;
+    const int cg0 = k0 % NCG, rb0 = k0 / NCG;
+    if (kt * KT + KT <= Tk) {
+      const char* wb = tb + ((int64_t)16 * rb0 * st + 32 * cg0) * 2;  // uniform
+      char* wl = tile + cg0 * 4096 + rb0 * 1024;
 #pragma unroll
-    for (int u = 0; u < KCH; ++u) {
-      const int c = tid + u * NT;
-      if (K_TOTAL % NT && c >= K_TOTAL) break;
-      const int key = c / DC, dc = c % DC;
-      const int tok = min(kt * KT + key, a.Tk - 1);
-      st.kr[u] = *reinterpret_cast<const u32x4*>(kb + tok * a.k_st + dc * 8);
-    }
+      for (int u = 0; u < NIW; ++u) {
+        const int du = NIW <= NCG ? 0 : u / NCG;  // row blocks past rb0
+        const int cu = NIW <= NCG ? u : u % NCG;  // column groups past cg0
+        load_lds16(wb + (int64_t)32 * du * st + 64 * cu, off, lds_addr(wl + cu * 4096 + du * 1024));
+      }
+    } else {
+      const int last = Tk - 1 - kt * KT;
 #pragma unroll
-    for (int u = 0; u < VUN; ++u) {
-      const int c = tid + u * NT;
-      if (V_TOTAL % NT && c >= V_TOTAL) break;
-      const int kg = c % (KT / 4), dc = c / (KT / 4);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const int tok = min(kt * KT + 4 * kg + kk, a.Tk - 1);
-        st.vr[u][kk] = *reinterpret_cast<const u32x4*>(vb + tok * a.v_st + dc * 8);
+      for (int u = 0; u < NIW; ++u) {
+        const int k = k0 + u;
+        const int cg = k % NCG, rb = k / NCG;
+        const int row = 16 * rb + (lane >> 2);
+        const int r = min(PERMUTE ? krow(row) : row, last);
+        load_lds16(tb + ((int64_t)r * st + 32 * cg + dma_col(lane)) * 2, lds_addr(tile + cg * 4096 + rb * 1024));
       }
     }
   }
 
-  static __device__ __forceinline__ void store(const Stage& st, elem_t* sK, elem_t* sVt, int tid) {
-#pragma unroll
-    for (int u = 0; u < KCH; ++u) {
-      const int c = tid + u * NT;
-      if (K_TOTAL % NT && c >= K_TOTAL) break;
-      const int key = c / DC, dc = c % DC;
-      *reinterpret_cast<u32x4*>(sK + krow(key) * KS + dc * 8) = st.kr[u];
+  // ---- fragments ----------------------------------------------------------------------
+  // Per-lane byte offsets of the fragment reads (tile-invariant).  The K offset of odd
+  // chunk pairs is k0 ^ 32 and the V^T offset of the upper key quad is (v0 + 256) ^ 16.
+  struct Frag {
+    int k0, v0;
+    __device__ __forceinline__ Frag(int lane) {
+      const int l32 = lane & 31, g = lane >> 5;
+      k0 = l32 * 64 + 16 * (g ^ ((l32 >> 2) & 3));
+      const int i = lane & 15, G = lane >> 4;
+      const int c4 = 2 * (G & 1) + ((i >> 1) & 1);
+      v0 = (8 * g + (i >> 2)) * 64 + 16 * (c4 ^ (2 * g)) + 8 * (i & 1);
     }
+  };
+
+  // A operand of S^T = K Q^T: row 32j + l32 of the staged K tile (key krow of it),
+  // columns 16cc + 8g .. +7.
+  static __device__ __forceinline__ u32x4 kfrag(const char* cK, const Frag& f, int j, int cc) {
+    const int off = (cc & 1) ? (f.k0 ^ 32) : f.k0;
+    return *reinterpret_cast<const u32x4*>(cK + 4096 * (cc >> 1) + 2048 * j + off);
+  }
+
+  static __device__ __forceinline__ u32x2 ds_tr16(const char* p) {
+    typedef short v4i16 __attribute__((ext_vector_type(4)));
+    const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
+    return __builtin_bit_cast(u32x2, r);
+  }
+
+  // A operand of O^T = V^T P^T: lane l holds d = 32dt + l32 of keys 32j + 16h + 8g + 0..7.
+  // ds_read_b64_tr_b16 gives lane i of each 16-lane group element e = the (i & 3)-th value
+  // at the address of lane 4e + (i >> 2); each lane addresses key (i >> 2) of a 4-key quad
+  // at columns 4(i & 3) of its 16-column group, so lane i receives column i of 4 keys.
+  static __device__ __forceinline__ u32x4 vfrag(const char* cV, const Frag& f, int j, int h, int dt) {
+    const char* p = cV + 4096 * dt + 2048 * j + 1024 * h;
+    const u32x2 lo = ds_tr16(p + f.v0);
+    const u32x2 hi = ds_tr16(p + ((f.v0 + 256) ^ 16));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  }
+
+  // B operand of S^T = K Q^T from a wave's staged Q ([cc][lane] 16 bytes: lane l holds row
+  // l32, columns 16cc + 8g .. +7).
+  static __device__ __forceinline__ u32x4 qfrag(const char* sQw, int lane, int cc) {
+    return *reinterpret_cast<const u32x4*>(sQw + cc * 1024 + lane * 16);
+  }
+
+  // ---- work items ---------------------------------------------------------------------
+  struct Item {
+    int g, l32, hf, hq;
+    const elem_t* qb;
+    const elem_t* kb;
+    const elem_t* vb;
+    const int32_t* prow;
+    int e0, n_tiles, tpb_mask;
+    bool cached;
+    int q_row0, q_abs_tile_max, q_abs_min;
+  };
+
+  // Sets up work item (qt, r, hs, b): query tile qt (64 rows) of CSR row r, batch b, head
+  // split hs.  Each wave owns 32 rows (half hf) of one query head; every K/V tile staged in
+  // LDS feeds all NW waves.  Caches the CSR row of the query tile in s_row (callers barrier
+  // before, so no wave still reads it).
+  static __device__ __forceinline__ Item setup(const PrefillArgs& a, int qt, int r, int hs, int b, int32_t* s_row) {
+    Item it;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    it.g = lane >> 5;
+    it.l32 = lane & 31;
+    const int hw = wave % HW;  // head within the workgroup
+    it.hf = wave / HW;         // 32-row half of the query tile
+    it.hq = r * a.heads_per_row + hs * HW + hw;
+    const int kvh = (r * a.heads_per_row + hs * HW) / (a.Hq / a.Hkv);  // shared by the waves
+    it.qb = a.q + b * a.q_sb + it.hq * a.q_sh;
+    it.kb = a.k + b * a.k_sb + kvh * a.k_sh;
+    it.vb = a.v + b * a.v_sb + kvh * a.v_sh;
+
+    // CSR row of this query tile; each block holds 2^tpb_log2 key tiles.
+    const int qblk = qt >> a.qpb_log2;
+    const int32_t* offs = a.offsets + r * a.offsets_stride;
+    it.prow = a.pairs + r * a.pairs_stride;
+    it.e0 = offs[qblk];
+    const int n_ent = offs[qblk + 1] - it.e0;
+    it.cached = n_ent <= ROW_CACHE;
+    if (it.cached)
+      for (int x = tid; x < n_ent; x += NT) s_row[x] = it.prow[it.e0 + x];
+    it.n_tiles = n_ent << a.tpb_log2;
+    it.tpb_mask = (1 << a.tpb_log2) - 1;
+    const int q_tile0 = qt * QTILE;
+    it.q_row0 = q_tile0 + QT * it.hf;  // this wave's first row
+    it.q_abs_tile_max = a.q_offset + min(a.Tq, q_tile0 + QTILE) - 1;
+    it.q_abs_min = a.q_offset + it.q_row0;  // this wave's first absolute position
+    return it;
+  }
+
+  // Rows of Q past T_q read a clamped (valid) row; their outputs are never stored.
+  static __device__ __forceinline__ const elem_t* q_src(const PrefillArgs& a, const Item& it) {
+    const int row = min(it.q_row0 + it.l32, a.Tq - 1);
+    return it.qb + (int64_t)row * a.q_st + 8 * it.g;
+  }
+
+  static __device__ __forceinline__ int tile_of(const PrefillArgs& a, const Item& it, const int32_t* s_row, int t) {
+    const int e = t >> a.tpb_log2;
+    // Two distinct loads (LDS cache, or a global read past ROW_CACHE entries); the global
+    // one is a relaxed atomic so the two are not merged into one flat load of a selected
+    // pointer (a flat load would also wait for the in-flight direct loads).
+    const int blk = it.cached ? s_row[e]
+                              : __hip_atomic_load(it.prow + it.e0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (blk << a.tpb_log2) + (t & it.tpb_mask);
+  }
+
+  // First tile at or after t that can contribute: tiles entirely past T_k or above the
+  // causal limit of the whole 64-row query tile are skipped, and so are negative ids
+  // (malformed schedules) rather than read.
+  static __device__ __forceinline__ int next_usable(const PrefillArgs& a, const Item& it, const int32_t* s_row,
+                                                    int t) {
+    for (; t < it.n_tiles; ++t) {
+      const int kt = tile_of(a, it, s_row, t);
+      if (kt >= 0 && kt * KT < a.Tk && kt * KT <= it.q_abs_tile_max) break;
+    }
+    return t;
+  }
+
+  // O / l written through this wave's 32 x D staging area in LDS (rows at 2D bytes, 16-byte
+  // chunk c of row r at position c ^ (r % (D/8))), then stored as 16-byte row pieces: each
+  // global store instruction writes whole contiguous rows.  The caller guarantees that no
+  // other wave uses `stage` (a barrier after the last read of the K/V buffers).
+  static __device__ __forceinline__ void epilogue(const PrefillArgs& a, const Item& it, int b,
+                                                  const f32x16 (&O)[D / 32], float l_run, char* stage, int lane) {
+    constexpr int NCH = D / 8;         // 16-byte chunks per row
+    constexpr int RPI = 1024 / (2 * D);  // rows per 1 KiB wave-wide read
+    const float lt = l_run + swap_halves(l_run);
+    const float inv = lt > 0.f ? 1.f / lt : 1.f;
 #pragma unroll
-    for (int u = 0; u < VUN; ++u) {
-      const int c = tid + u * NT;
-      if (V_TOTAL % NT && c >= V_TOTAL) break;
-      const int kg = c % (KT / 4), dc = c / (KT / 4);
+    for (int dt = 0; dt < D / 32; ++dt)
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {  // d = dc*8 + 2w (low halves) and 2w+1 (high halves)
-        const uint32_t x0 = st.vr[u][0][w], x1 = st.vr[u][1][w];
-        const uint32_t x2 = st.vr[u][2][w], x3 = st.vr[u][3][w];
-        const u32x2 even = {(x0 & 0xffffu) | (x1 << 16), (x2 & 0xffffu) | (x3 << 16)};
-        const u32x2 odd = {(x0 >> 16) | (x1 & 0xffff0000u), (x2 >> 16) | (x3 & 0xffff0000u)};
-        *reinterpret_cast<u32x2*>(sVt + (dc * 8 + 2 * w) * VS + 4 * kg) = even;
-        *reinterpret_cast<u32x2*>(sVt + (dc * 8 + 2 * w + 1) * VS + 4 * kg) = odd;
+      for (int rq = 0; rq < 4; ++rq) {  // d = 32dt + 8rq + 4g + 0..3: chunk 4dt + rq, half g
+        const int c = 4 * dt + rq;
+        const u32x2 w = {E::pack2f(O[dt][4 * rq] * inv, O[dt][4 * rq + 1] * inv),
+                         E::pack2f(O[dt][4 * rq + 2] * inv, O[dt][4 * rq + 3] * inv)};
+        *reinterpret_cast<u32x2*>(stage + it.l32 * 2 * D + 16 * (c ^ (it.l32 & (NCH - 1))) + 8 * it.g) = w;
       }
+    // The wave reads back what its own lanes wrote: LDS executes one wave's accesses in
+    // order, so only the compiler must keep the order.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    elem_t* ob = a.o + b * a.o_sb + it.hq * a.o_sh;
+#pragma unroll
+    for (int k = 0; k < QT / RPI; ++k) {
+      const int row = RPI * k + lane / NCH;
+      const int p = lane % NCH;
+      const u32x4 w = *reinterpret_cast<const u32x4*>(stage + row * 2 * D + 16 * p);
+      const int qrow = it.q_row0 + row;
+      if (qrow < a.Tq) *reinterpret_cast<u32x4*>(ob + (int64_t)qrow * a.o_st + 8 * (p ^ (row & (NCH - 1)))) = w;
     }
   }
 
+  // ---- one tile at a time (one- and two-head workgroups) -------------------------------
   // Online softmax over the 32-key half j of the current tile for this wave's 32 rows.
   // Scores are raw; p = 2^(s*c - m_ref).  Returns the P^T operands of the two 16-key chunks.
   template <bool MASK>
@@ -181,14 +388,13 @@ struct Prefill {
     float ls = 0.f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      elem_t pe[8];
+      float pf[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float p = fast_exp2(fmaf(S[8 * h + e], c, neg_m));
-        ls += p;
-        pe[e] = E::from_f32(p);
+        pf[e] = fast_exp2(fmaf(S[8 * h + e], c, neg_m));
+        ls += pf[e];
       }
-      P[h] = u32x4{pack2(pe[0], pe[1]), pack2(pe[2], pe[3]), pack2(pe[4], pe[5]), pack2(pe[6], pe[7])};
+      P[h] = u32x4{E::pack2f(pf[0], pf[1]), E::pack2f(pf[2], pf[3]), E::pack2f(pf[4], pf[5]), E::pack2f(pf[6], pf[7])};
     }
     l_run += ls;
   }
@@ -196,97 +402,46 @@ struct Prefill {
   // One 64-key tile: S^T = K Q^T per 32-key half, softmax, O^T += V^T P^T.  The softmax of
   // one half can run under the matrix instructions of the other half.
   template <bool MASK>
-  static __device__ __forceinline__ void tile(const elem_t* cK, const elem_t* cV, const u32x4 (&qf)[D / 16],
-                                              f32x16 (&O)[D / 32], float& m_ref, float& l_run, float c,
-                                              int lim, int l32, int g) {
+  static __device__ __forceinline__ void tile(const char* cK, const char* cV, const Frag& f,
+                                              const u32x4 (&qf)[D / 16], f32x16 (&O)[D / 32], float& m_ref,
+                                              float& l_run, float c, int lim) {
     // The two key halves are independent accumulation chains; alternating them keeps the
     // matrix pipe busy while each MFMA waits for its predecessor's result.
     f32x16 S[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-    for (int cc = 0; cc < D / 16; ++cc) {
+    for (int cc = 0; cc < D / 16; ++cc)
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(cK + (32 * j + l32) * KS + 16 * cc + 8 * g);
-        S[j] = E::mfma32(kf, qf[cc], S[j]);
-      }
-    }
+      for (int j = 0; j < 2; ++j) S[j] = E::mfma32(kfrag(cK, f, j, cc), qf[cc], S[j]);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       u32x4 P[2];
       softmax_half<MASK>(S[j], P, O, m_ref, l_run, c, lim, j);
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int kbase = 32 * j + 16 * h + 8 * g;
+      for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          const u32x4 vf = *reinterpret_cast<const u32x4*>(cV + (32 * dt + l32) * VS + kbase);
-          O[dt] = E::mfma32(vf, P[h], O[dt]);
-        }
-      }
+        for (int dt = 0; dt < D / 32; ++dt) O[dt] = E::mfma32(vfrag(cV, f, j, h, dt), P[h], O[dt]);
     }
   }
 
-  // Processes one work item: query tile qt (64 rows) of CSR row r, batch b, head split hs.
-  // Each wave owns 32 rows (half hf) of one query head; every K/V tile staged in LDS feeds
-  // all NW waves.  s_row must not be in use by other waves (callers barrier before).
-  static __device__ __forceinline__ void item(const PrefillArgs& a, int qt, int r, int hs, int b,
-                                              elem_t (*sK)[KT * KS], elem_t (*sVt)[D * VS],
+  // One work item, one tile at a time: the next tile's direct loads run under the current
+  // tile's compute (double buffer), or after it (single buffer).
+  static __device__ __forceinline__ void item(const PrefillArgs& a, int qt, int r, int hs, int b, char* sKV,
                                               int32_t* s_row) {
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int g = lane >> 5;
-    const int l32 = lane & 31;
-    const int hw = wave % HW;        // head within the workgroup
-    const int hf = wave / HW;        // 32-row half of the query tile
-    const int hq = r * a.heads_per_row + hs * HW + hw;
-    const int kvh = (r * a.heads_per_row + hs * HW) / (a.Hq / a.Hkv);  // shared by the waves
-
-    const elem_t* qb = a.q + b * a.q_sb + hq * a.q_sh;
-    const elem_t* kb = a.k + b * a.k_sb + kvh * a.k_sh;
-    const elem_t* vb = a.v + b * a.v_sb + kvh * a.v_sh;
-
-    // CSR row of this query tile, cached in LDS; each block holds 2^tpb_log2 key tiles.
-    const int qblk = qt >> a.qpb_log2;
-    const int32_t* offs = a.offsets + r * a.offsets_stride;
-    const int32_t* prow = a.pairs + r * a.pairs_stride;
-    const int e0 = offs[qblk];
-    const int n_ent = offs[qblk + 1] - e0;
-    const bool cached = n_ent <= ROW_CACHE;
-    if (cached)
-      for (int x = tid; x < n_ent; x += NT) s_row[x] = prow[e0 + x];
-    const int n_tiles = n_ent << a.tpb_log2;
-    const int tpb_mask = (1 << a.tpb_log2) - 1;
-    const int q_tile0 = qt * QTILE;
-    const int q_row0 = q_tile0 + QT * hf;            // this wave's first row
-    const int q_abs_tile_max = a.q_offset + min(a.Tq, q_tile0 + QTILE) - 1;
-    const int q_abs_min = a.q_offset + q_row0;       // this wave's first absolute position
-
+    char* sK = sKV;
+    char* sV = sKV + NBK * TILE_BYTES;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const Item it = setup(a, qt, r, hs, b, s_row);
     // Q^T as the B operand of S^T = K Q^T: lane holds row l32, d = 16c + 8g .. +7.
-    // Rows past T_q read a clamped (valid) row; their outputs are never stored.
     u32x4 qf[D / 16];
     {
-      const int row = min(q_row0 + l32, a.Tq - 1);
+      const elem_t* qs = q_src(a, it);
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c)
-        qf[c] = *reinterpret_cast<const u32x4*>(qb + row * a.q_st + 16 * c + 8 * g);
+      for (int c = 0; c < D / 16; ++c) qf[c] = *reinterpret_cast<const u32x4*>(qs + 16 * c);
     }
+    const Frag f(lane);
+    const DmaLane dl(a, lane);
     __syncthreads();  // s_row visible
-
-    auto tile_of = [&](int t) {
-      const int e = t >> a.tpb_log2;
-      const int blk = cached ? s_row[e] : prow[e0 + e];
-      return (blk << a.tpb_log2) + (t & tpb_mask);
-    };
-    // Tiles entirely past T_k or above the causal limit of the whole 64-row tile contribute
-    // nothing; negative ids (malformed schedules) are skipped rather than read.
-    auto next_usable = [&](int t) {
-      for (; t < n_tiles; ++t) {
-        const int kt = tile_of(t);
-        if (kt >= 0 && kt * KT < a.Tk && kt * KT <= q_abs_tile_max) break;
-      }
-      return t;
-    };
 
     f32x16 O[D / 32];
 #pragma unroll
@@ -295,63 +450,252 @@ struct Prefill {
     float l_run = 0.f;  // this lane's half of the row sum
     const float c = a.scale_log2;
 
-    Stage st;
-    int t = next_usable(0);
+    int t = next_usable(a, it, s_row, 0);
     int buf = 0;
-    if (t < n_tiles) {
-      load(st, kb, vb, a, tile_of(t), tid);
-      store(st, sK[0], sVt[0], tid);
+    if (t < it.n_tiles) {
+      const int kt = tile_of(a, it, s_row, t);
+      dma<true>(it.kb, a.k_st, dl.k, sK, kt, a.Tk, wave, lane);
+      dma<false>(it.vb, a.v_st, dl.v, sV, kt, a.Tk, wave, lane);
     }
+    wait_dma();
     __syncthreads();
 
-    while (t < n_tiles) {
-      const int kt = tile_of(t);
-      const int tn = next_usable(t + 1);
-      if (PREFETCH && tn < n_tiles) load(st, kb, vb, a, tile_of(tn), tid);
-      const elem_t* cK = sK[buf];
-      const elem_t* cV = sVt[buf];
+    while (t < it.n_tiles) {
+      const int kt = tile_of(a, it, s_row, t);
+      const int tn = next_usable(a, it, s_row, t + 1);
+      if (NBK == 2 && tn < it.n_tiles) {
+        const int ktn = tile_of(a, it, s_row, tn);
+        dma<true>(it.kb, a.k_st, dl.k, sK + (buf ^ 1) * TILE_BYTES, ktn, a.Tk, wave, lane);
+        dma<false>(it.vb, a.v_st, dl.v, sV + (buf ^ 1) * TILE_BYTES, ktn, a.Tk, wave, lane);
+      }
+      const char* cK = sK + buf * TILE_BYTES;
+      const char* cV = sV + buf * TILE_BYTES;
 
       // A wave whose 32 rows all precede the tile skips it (the other half may not).
-      if (kt * KT <= q_abs_min + QT - 1) {
-        const bool need_mask = (kt * KT + KT - 1 > q_abs_min) || (kt * KT + KT > a.Tk);
-        const int lim = min(q_abs_min + l32, a.Tk - 1) - kt * KT - 8 * g;
+      if (kt * KT <= it.q_abs_min + QT - 1) {
+        const bool need_mask = (kt * KT + KT - 1 > it.q_abs_min) || (kt * KT + KT > a.Tk);
+        const int lim = min(it.q_abs_min + it.l32, a.Tk - 1) - kt * KT - 8 * it.g;
         if (need_mask)
-          tile<true>(cK, cV, qf, O, m_ref, l_run, c, lim, l32, g);
+          tile<true>(cK, cV, f, qf, O, m_ref, l_run, c, lim);
         else
-          tile<false>(cK, cV, qf, O, m_ref, l_run, c, lim, l32, g);
+          tile<false>(cK, cV, f, qf, O, m_ref, l_run, c, lim);
       }
 
-      if (tn < n_tiles) {
-        if (PREFETCH) {
-          store(st, sK[buf ^ 1], sVt[buf ^ 1], tid);
-        } else {
-          __syncthreads();  // single buffer: every wave is done reading it
-          Stage st2;
-          load(st2, kb, vb, a, tile_of(tn), tid);
-          store(st2, sK[0], sVt[0], tid);
-        }
+      if (NBK == 1 && tn < it.n_tiles) {
+        __syncthreads();  // single buffer: every wave is done reading it
+        const int ktn = tile_of(a, it, s_row, tn);
+        dma<true>(it.kb, a.k_st, dl.k, sK, ktn, a.Tk, wave, lane);
+        dma<false>(it.vb, a.v_st, dl.v, sV, ktn, a.Tk, wave, lane);
       }
+      wait_dma();
       __syncthreads();
-      if (PREFETCH) buf ^= 1;
+      if (NBK == 2) buf ^= 1;
       t = tn;
     }
+    // Every wave has passed the last barrier: the K/V buffers are free for the staging.
+    epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
+  }
 
-    // ---- epilogue: O / l, one row per lane column ---------------------------------------
-    const float lt = l_run + swap_halves(l_run);
-    const float inv = lt > 0.f ? 1.f / lt : 1.f;
-    const int row = q_row0 + l32;
-    if (row < a.Tq) {
-      elem_t* orow = a.o + b * a.o_sb + hq * a.o_sh + row * a.o_st;
+  // ---- software-pipelined loop (four-head workgroups) ----------------------------------
+  // Masks (causal / past T_k, branch-free) one tile's S^T and returns its scaled row max.
+  // lim = last visible key offset in the tile minus 8g (past the tile when nothing is masked).
+  static __device__ __forceinline__ float mask_rowmax(f32x16 (&S)[2], int lim, float c) {
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int d0 = 32 * dt + 8 * rq + 4 * g;
-          const u32x2 w = {pack2(E::from_f32(O[dt][4 * rq] * inv), E::from_f32(O[dt][4 * rq + 1] * inv)),
-                           pack2(E::from_f32(O[dt][4 * rq + 2] * inv), E::from_f32(O[dt][4 * rq + 3] * inv))};
-          *reinterpret_cast<u32x2*>(orow + d0) = w;
-        }
+      for (int rr = 0; rr < 16; ++rr)
+        S[j][rr] = (32 * j + 16 * (rr >> 3) + (rr & 7) > lim) ? -__builtin_inff() : S[j][rr];
+    float mx = S[0][0];
+#pragma unroll
+    for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, S[0][rr]);
+#pragma unroll
+    for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, S[1][rr]);
+    mx = fmaxf(mx, swap_halves(mx));
+    return mx * c;  // -inf stays -inf (c > 0)
+  }
+
+  // Raises the row reference when the tile's max exceeds it by more than 2^RESCALE_LOG2
+  // (rare; rescales O and l) and returns -m_ref for the exponent.
+  static __device__ __forceinline__ float update_ref(float m_tile, float& m_ref, float& l_run,
+                                                     f32x16 (&O)[D / 32]) {
+    float m = m_ref == -__builtin_inff() ? m_tile : m_ref;
+    if (__any(m_tile > m + RESCALE_LOG2)) {
+      const float m_new = fmaxf(m, m_tile);
+      const float alpha = m_new == -__builtin_inff() ? 1.f : fast_exp2(m - m_new);
+      m = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) O[dt] *= alpha;
     }
+    m_ref = m;
+    return m == -__builtin_inff() ? 0.f : -m;
+  }
+
+  // Same work item as item(), with the tile loop software-pipelined: each step computes the
+  // probabilities of tile i while the matrix cores already run S^T = K Q^T of tile i+1,
+  // then O^T += V^T P^T of tile i while the VALU reduces the row max of tile i+1.
+  // Meanwhile the direct loads fetch K of tile i+2 (three K buffers) and V of tile i+1 (two
+  // V buffers).  Tiles that lie wholly after this wave's rows cost matrix work but add
+  // p == 0.
+  static __device__ __forceinline__ void item_pipelined(const PrefillArgs& a, int qt, int r, int hs, int b,
+                                                        char* sKV, char* sQ, int32_t* s_row) {
+    char* sK = sKV;
+    char* sV = sKV + NBK * TILE_BYTES;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const Item it = setup(a, qt, r, hs, b, s_row);
+    const char* sQw = sQ + wave * WAVE_BYTES;
+    {  // Q^T operand of this wave into LDS, in fragment order
+      const elem_t* qs = q_src(a, it);
+#pragma unroll
+      for (int cc = 0; cc < D / 16; ++cc) load_lds16(qs + 16 * cc, lds_addr(sQw + cc * 1024));
+    }
+    const Frag f(lane);
+    const DmaLane dl(a, lane);
+    // lim of tile kt: min(q_abs, T_k - 1) - kt*KT - 8g (past the tile when no key is masked)
+    const int lim0 = min(it.q_abs_min + it.l32, a.Tk - 1) - 8 * it.g;
+    __syncthreads();  // s_row visible
+
+    f32x16 O[D / 32];
+#pragma unroll
+    for (int dt = 0; dt < D / 32; ++dt) O[dt] = f32x16{};
+    float m_ref = -__builtin_inff();
+    float l_run = 0.f;
+    const float c = a.scale_log2;
+    const int n_tiles = it.n_tiles;
+
+    // Prime: K of tiles t0, t1 in K buffers 0, 1 and V of t0 in V buffer 0; S^T and row
+    // max of t0.
+    int t_cur = next_usable(a, it, s_row, 0);
+    int t_nxt = t_cur < n_tiles ? next_usable(a, it, s_row, t_cur + 1) : n_tiles;
+    int kt_cur = t_cur < n_tiles ? tile_of(a, it, s_row, t_cur) : 0;
+    int kt_nxt = t_nxt < n_tiles ? tile_of(a, it, s_row, t_nxt) : 0;
+    if (t_cur < n_tiles) {
+      dma<true>(it.kb, a.k_st, dl.k, sK, kt_cur, a.Tk, wave, lane);
+      dma<false>(it.vb, a.v_st, dl.v, sV, kt_cur, a.Tk, wave, lane);
+    }
+    if (t_nxt < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+    wait_dma();
+    __syncthreads();
+    f32x16 S[2] = {f32x16{}, f32x16{}};  // scores of the current tile
+    float mt_cur = -__builtin_inff();
+    if (t_cur < n_tiles) {
+#pragma unroll
+      for (int cc = 0; cc < D / 16; ++cc) {
+        const u32x4 qv = qfrag(sQw, lane, cc);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) S[j] = E::mfma32(kfrag(sK, f, j, cc), qv, S[j]);
+      }
+      mt_cur = mask_rowmax(S, lim0 - kt_cur * KT, c);
+    }
+
+    int kb_cur = 0;  // K buffer of the current tile (tile t_nxt's is kb_cur + 1 mod 3)
+    int vb_cur = 0;  // V buffer of the current tile
+    // One pipeline step on the tile in S (this tile) while filling Sn (next tile).
+    while (t_cur < n_tiles) {
+      const int kb_nxt = kb_cur == 2 ? 0 : kb_cur + 1;
+      const int kb_nn = kb_nxt == 2 ? 0 : kb_nxt + 1;
+      const int t_nn = t_nxt < n_tiles ? next_usable(a, it, s_row, t_nxt + 1) : n_tiles;
+      const int kt_nn = t_nn < n_tiles ? tile_of(a, it, s_row, t_nn) : 0;
+      if (t_nn < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + kb_nn * TILE_BYTES, kt_nn, a.Tk, wave, lane);
+      if (t_nxt < n_tiles) dma<false>(it.vb, a.v_st, dl.v, sV + (vb_cur ^ 1) * TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+      const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
+      u32x4 P[2][2];
+      const char* cV = sV + vb_cur * TILE_BYTES;
+      const char* cK = sK + kb_nxt * TILE_BYTES;
+      // Branch-free on purpose: after the last tile the QK half runs on a stale K buffer
+      // (no direct load is in flight then) and its result is dropped.  A separate last-tile
+      // path would let the compiler merge the two copies of the exponentials ahead of the
+      // branch, which undoes the interleaving.
+      //
+      // Block A: QK of the next tile (D/8 MFMAs; K fragments read three MFMAs ahead, Q
+      // fragments two chunk pairs ahead) with this tile's probabilities spread over it.
+      // The sched_barrier fences keep the order as written: one MFMA, its LDS reads, its
+      // share of the VALU work.
+      constexpr int NQ = D / 8;    // QK MFMAs per tile: i -> (key half j = i % 2, cc = i / 2)
+      constexpr int PE = 32 / NQ;  // probabilities per QK MFMA
+      auto kfr = [&](int i) { return kfrag(cK, f, i & 1, i >> 1); };
+      u32x4 kf[3] = {kfr(0), kfr(1), kfr(2)};
+      u32x4 qv[2] = {qfrag(sQw, lane, 0), qfrag(sQw, lane, 1)};
+      f32x16 Sn[2] = {f32x16{}, f32x16{}};
+      float ls = 0.f;
+      uint32_t pw[2][2][4];
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NQ; ++i) {
+        Sn[i & 1] = E::mfma32(kf[i % 3], qv[(i >> 1) & 1], Sn[i & 1]);
+        if (i + 3 < NQ) kf[i % 3] = kfr(i + 3);
+        if ((i & 1) && (i >> 1) + 2 < D / 16) qv[(i >> 1) & 1] = qfrag(sQw, lane, (i >> 1) + 2);
+#pragma unroll
+        for (int u = 0; u < PE; u += 2) {
+          const int x = PE * i + u;
+          const int j = x >> 4, rr = x & 15;
+          const float p0 = fast_exp2(fmaf(S[j][rr], c, neg_m));
+          const float p1 = fast_exp2(fmaf(S[j][rr + 1], c, neg_m));
+          ls += p0 + p1;
+          uint32_t w = E::pack2f(p0, p1);
+          // Pins the computation here: without it the compiler sinks the exponentials past
+          // the mask branch to their use in block B.
+          asm volatile("" : "+v"(w), "+v"(ls));
+          pw[j][rr >> 3][(rr & 7) >> 1] = w;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      l_run += ls;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) P[j][h] = u32x4{pw[j][h][0], pw[j][h][1], pw[j][h][2], pw[j][h][3]};
+
+      // Causal / T_k mask of the next tile, only where it cuts into the tile (uniform per
+      // wave; about one tile in a row's window).
+      const int kbase_n = kt_nxt * KT;
+      if (kbase_n + KT - 1 > it.q_abs_min || kbase_n + KT > a.Tk) {
+        const int lim = lim0 - kbase_n;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int rr = 0; rr < 16; ++rr)
+            Sn[j][rr] = (32 * j + 16 * (rr >> 3) + (rr & 7) > lim) ? -__builtin_inff() : Sn[j][rr];
+      }
+
+      // Block B: PV of this tile (D/8 MFMAs; V fragments read two MFMAs ahead) with the
+      // next tile's row max spread over it.
+      constexpr int NP = D / 8;  // PV MFMAs: i -> (dt = i % (D/32), h, j)
+      constexpr int ND = D / 32;
+      constexpr int ME = 32 / NP;  // scores reduced per PV MFMA
+      auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
+      u32x4 vf[2] = {vfr(0), vfr(1)};
+      float mx = -__builtin_inff();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        O[i % ND] = E::mfma32(vf[i & 1], P[i / (2 * ND)][(i / ND) & 1], O[i % ND]);
+        if (i + 2 < NP) vf[i & 1] = vfr(i + 2);
+#pragma unroll
+        for (int u = 0; u < ME; ++u) {
+          const int x = ME * i + u;
+          mx = fmaxf(mx, Sn[x >> 4][x & 15]);
+        }
+        asm volatile("" : "+v"(mx));  // keeps the reduction spread over the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      mx = fmaxf(mx, swap_halves(mx));
+      mt_cur = mx * c;
+
+      S[0] = Sn[0];
+      S[1] = Sn[1];
+      wait_dma();
+      __syncthreads();
+      t_cur = t_nxt;
+      kt_cur = kt_nxt;
+      t_nxt = t_nn;
+      kt_nxt = kt_nn;
+      kb_cur = kb_nxt;
+      vb_cur ^= 1;
+    }
+    // Every wave has passed the last barrier: the K/V buffers are free for the staging.
+    epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
   }
 
   // Item index -> (qt, r, hs, b), the heaviest (latest) query tiles first.
@@ -365,9 +709,19 @@ struct Prefill {
     b = rem / a.head_splits;
   }
 
+  static __device__ __forceinline__ void process(const PrefillArgs& a, int v, char* sKV, char* sQ,
+                                                 int32_t* s_row) {
+    int qt, r, hs, b;
+    decode_item(a, v, qt, r, hs, b);
+    if constexpr (PIPE)
+      item_pipelined(a, qt, r, hs, b, sKV, sQ, s_row);
+    else
+      item(a, qt, r, hs, b, sKV, s_row);
+  }
+
   static __device__ void run(const PrefillArgs& a) {
-    __shared__ __attribute__((aligned(16))) elem_t sK[NBUF][KT * KS];
-    __shared__ __attribute__((aligned(16))) elem_t sVt[NBUF][D * VS];
+    __shared__ __attribute__((aligned(16))) char sKV[LDS_KV];
+    __shared__ __attribute__((aligned(16))) char sQ[LDS_Q];
     __shared__ int32_t s_row[ROW_CACHE];
     __shared__ int s_item;
     const int n_items = a.ntq * a.R * a.B * a.head_splits;
@@ -382,23 +736,20 @@ struct Prefill {
       const int xcd = blockIdx.x % N_XCD, seq = blockIdx.x / N_XCD;
       const int v = ((seq / chunk) * N_XCD + xcd) * chunk + seq % chunk;
       if (v >= n_items) return;  // padding workgroup of the last round
-      int qt, r, hs, b;
-      decode_item(a, v, qt, r, hs, b);
-      item(a, qt, r, hs, b, sK, sVt, s_row);
+      process(a, v, sKV, sQ, s_row);
       return;
     }
 
     // Persistent: claim items from a counter until none is left.  The last workgroup to
-    // finish resets the counter pair to zero for the next launch on the stream.
+    // finish resets the counter pair to zero for the next launch on the stream.  The
+    // barriers also separate one item's epilogue (LDS staging) from the next item's loads.
     for (;;) {
       if (threadIdx.x == 0) s_item = (int)atomicAdd(&a.counter[0], 1u);
       __syncthreads();
       const int v = s_item;
       __syncthreads();
       if (v >= n_items) break;
-      int qt, r, hs, b;
-      decode_item(a, v, qt, r, hs, b);
-      item(a, qt, r, hs, b, sK, sVt, s_row);
+      process(a, v, sKV, sQ, s_row);
     }
     if (threadIdx.x == 0 && atomicAdd(&a.counter[1], 1u) == gridDim.x - 1) {
       atomicExch(&a.counter[0], 0u);
@@ -499,6 +850,9 @@ extern "C" int sa_prefill(int dtype,
     if (s % 8) return set_error(SA_E_ALIGN, "sa_prefill: stride %lld is not a multiple of 8 elements", (long long)s);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
     return set_error(SA_E_ALIGN, "sa_prefill: tensor base pointers must be 16-byte aligned");
+  if (k_st < 0 || v_st < 0 || k_st > MAX_KV_STRIDE || v_st > MAX_KV_STRIDE)
+    return set_error(SA_E_SHAPE, "sa_prefill: K/V token strides %lld, %lld outside [0, %lld]", (long long)k_st,
+                     (long long)v_st, (long long)MAX_KV_STRIDE);
 
   PrefillArgs a;
   a.q = static_cast<const elem_t*>(q);

@@ -14,6 +14,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -34,6 +37,10 @@ struct Elem<true> {
   static __device__ __forceinline__ elem_t from_f32(float f) {
     return __builtin_bit_cast(elem_t, static_cast<__bf16>(f));
   }
+  // from_f32(lo) | from_f32(hi) << 16 in one v_cvt_pk_bf16_f32.
+  static __device__ __forceinline__ uint32_t pack2f(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+  }
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
@@ -47,6 +54,10 @@ struct Elem<false> {
   }
   static __device__ __forceinline__ elem_t from_f32(float f) {
     return __builtin_bit_cast(elem_t, static_cast<_Float16>(f));
+  }
+  // from_f32(lo) | from_f32(hi) << 16.
+  static __device__ __forceinline__ uint32_t pack2f(float lo, float hi) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, f16x2));
   }
   static __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
