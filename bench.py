@@ -39,8 +39,10 @@ PAIR_FLOP = 4 * BS * BS     # x head_dim
 def parse():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    # The shader clock ramps up over the first tens of milliseconds of sustained load; the
+    # default warm-up (about 0.1 s of prefill) lets timing start at steady clocks.
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--only", choices=("all", "prefill", "decode"), default="all",
                     help="restrict to one kernel (for profiler runs)")
     ap.add_argument("--decode-splits", type=int, default=0, help="0 = time 1 and 2, keep the faster")

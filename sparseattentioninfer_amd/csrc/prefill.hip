@@ -620,6 +620,10 @@ struct Prefill {
       f32x16 Sn[2] = {f32x16{}, f32x16{}};
       float ls = 0.f;
       uint32_t pw[2][2][4];
+      // The two waves of a SIMD run the same step; raising the priority of the one in the
+      // VALU-heavy block A lets its exponentials go first while the other wave's matrix
+      // instructions fill the MFMA pipe (about 5% faster than equal priorities).
+      __builtin_amdgcn_s_setprio(1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
@@ -667,6 +671,7 @@ struct Prefill {
       auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
       u32x4 vf[2] = {vfr(0), vfr(1)};
       float mx = -__builtin_inff();
+      __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NP; ++i) {
