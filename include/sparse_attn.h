@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 2
+#define SA_ABI_VERSION 3
 
 /* element types */
 #define SA_DTYPE_BF16 0
@@ -69,9 +69,15 @@ const char* sa_last_error(void);
  * probabilities are rounded to the element type before the PV product, as in
  * the reference kernel (:147).
  *
- * block_size: 64 or 128 (the CSR granularity; the kernel tiles by 64).
+ * block_size: 64 or 128 (the CSR granularity; the kernel tiles by 64), or 16
+ * or 32 with a tile schedule: pairs/offsets then list the 64-key tiles of
+ * each 64-row query tile (as sa_csr_to_tiles writes them) and tile_masks,
+ * laid out like pairs with row stride tile_masks_stride, holds each entry's
+ * retained block_size x block_size sub-blocks: bit sr * (64 / block_size) + sc
+ * for query sub-block sr and key sub-block sc of the tile.  tile_masks must be
+ * NULL for block sizes 64 and 128.
  * head_dim D: 64 or 128.  nqb = number of CSR query blocks (offsets has
- * nqb + 1 entries per row), nqb == ceil(T_q / block_size).
+ * nqb + 1 entries per row), nqb == ceil(T_q / max(block_size, 64)).
  *
  * workspace (optional, sa_prefill_workspace_bytes() bytes, 4-byte aligned):
  * with it the kernel runs one persistent workgroup per resident slot that
@@ -87,6 +93,7 @@ int sa_prefill(int dtype,
                void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
                const int32_t* pairs, int64_t pairs_stride,
                const int32_t* offsets, int64_t offsets_stride,
+               const int32_t* tile_masks, int64_t tile_masks_stride,
                int csr_rows, int nqb,
                int B, int Hq, int Hkv, int T_q, int T_k, int D,
                int block_size, int q_offset, float sm_scale,
@@ -95,6 +102,32 @@ int sa_prefill(int dtype,
 
 /* Bytes of the optional sa_prefill workspace (a counter pair). */
 int64_t sa_prefill_workspace_bytes(void);
+
+/*
+ * Regroups a CSR schedule of block size 16 or 32 -- the granularity of the
+ * reference's BigBird layouts, whose CSR block is the next power of two of at
+ * least 16 (sparse_attentions/patterns/bigbird_pattern.py:99-101, :233) --
+ * into the tile schedule that
+ * sa_prefill takes for those block sizes.  One output row per input row.
+ * Query tile qt holds query blocks s*qt .. s*qt + s - 1 (s = 64 / block_size);
+ * its entries, ascending, are the key tiles kt = kb / s holding a retained
+ * block kb of any of those query blocks, each with its sub-block mask.
+ * Outputs: tile_pairs and tile_masks [rows, width] (row stride tile_stride,
+ * zero padded), tile_offsets [rows, ceil(nqb / s) + 1] (row stride
+ * tile_offsets_stride).  The ids of each query block must ascend, as the
+ * reference's CSR promises (sparse_attentions/patterns/base.py:48); negative
+ * ids are dropped.  *status, a device int the caller zeroes, receives bit 0
+ * if a row needed more than width tiles (never for a well-formed CSR: a row
+ * has no more tiles than entries, so the input's pairs width suffices) and
+ * bit 1 if some query block's ids did not ascend; either makes the schedule
+ * unusable.  Nothing is synchronised: read *status after the stream.
+ */
+int sa_csr_to_tiles(const int32_t* pairs, int64_t pairs_stride,
+                    const int32_t* offsets, int64_t offsets_stride,
+                    int rows, int nqb, int block_size,
+                    int32_t* tile_pairs, int32_t* tile_masks, int64_t tile_stride, int64_t width,
+                    int32_t* tile_offsets, int64_t tile_offsets_stride,
+                    int* status, void* stream);
 
 /*
  * Sparse decode: one new query token per sequence against a KV cache, reading

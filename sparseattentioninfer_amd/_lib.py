@@ -11,7 +11,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 
@@ -32,6 +32,7 @@ SIGNATURES = {
         _vp, _i64, _i64, _i64,
         _vp, _i64,
         _vp, _i64,
+        _vp, _i64,
         _i32, _i32,
         _i32, _i32, _i32, _i32, _i32, _i32,
         _i32, _i32, _f32,
@@ -39,6 +40,15 @@ SIGNATURES = {
         _vp,
     ]),
     "sa_prefill_workspace_bytes": (_i64, []),
+    "sa_csr_to_tiles": (_i32, [
+        _vp, _i64,
+        _vp, _i64,
+        _i32, _i32, _i32,
+        _vp, _vp, _i64, _i64,
+        _vp, _i64,
+        _vp,
+        _vp,
+    ]),
     "sa_decode": (_i32, [
         _i32,
         _vp, _i64, _i64,

@@ -17,6 +17,11 @@ Differences from the reference, all deliberate:
   query heads of each KV group, letting one K/V tile feed all of them.
 * ``kind == "dense"`` runs the kernels over a full causal schedule
   (bottom-right aligned: the query is the last ``T_q`` positions).
+
+Schedules derived from a pattern's tensors (the CSR of a padded list, the
+64 x 64 tile schedule of a block-16/32 CSR) are computed once and reused while
+the same tensors, unmodified, come back -- the reference's patterns hand every
+layer the same metadata.
 """
 from __future__ import annotations
 
@@ -27,6 +32,33 @@ from ..patterns.base import PatternMetadata, block_mask_to_csr, kv_block_list_to
 from .base import AttentionBackend
 
 _DENSE_BLOCK = 64
+_DERIVED_CACHE_SIZE = 8
+
+
+class _DerivedCache:
+    """Small LRU of schedules derived from tensors.
+
+    An entry holds its source tensors, so their memory cannot be reused by
+    another tensor while it is cached; it is valid while the same objects come
+    back with unchanged version counters (no in-place writes since).
+    """
+
+    def __init__(self, size: int = _DERIVED_CACHE_SIZE):
+        self._size = size
+        self._entries: list = []   # (sources, versions, extra key, value), most recent last
+
+    def get(self, sources: tuple, extra, make):
+        versions = tuple(t._version for t in sources)
+        for i, (src, ver, ex, val) in enumerate(self._entries):
+            if ex == extra and ver == versions and len(src) == len(sources) \
+                    and all(a is b for a, b in zip(src, sources)):
+                self._entries.append(self._entries.pop(i))
+                return val
+        val = make()
+        self._entries.append((sources, versions, extra, val))
+        if len(self._entries) > self._size:
+            self._entries.pop(0)
+        return val
 
 
 class HipBlockSparseBackend(AttentionBackend):
@@ -36,7 +68,8 @@ class HipBlockSparseBackend(AttentionBackend):
         self._last_actual_backend = "unknown"
         self.last_kernel = None          # "prefill" or "decode" after a forward
         self._dense_cache: dict = {}
-        self._list_cache: dict = {}
+        self._list_cache = _DerivedCache()
+        self._tile_cache = _DerivedCache()
 
     @property
     def actual_backend(self) -> str:
@@ -54,10 +87,13 @@ class HipBlockSparseBackend(AttentionBackend):
         return self._dense_cache[key]
 
     def _list_schedule(self, kv_block_list: torch.Tensor) -> tuple:
-        key = (kv_block_list.data_ptr(), tuple(kv_block_list.shape), kv_block_list._version)
-        if key not in self._list_cache:
-            self._list_cache[key] = kv_block_list_to_pairs(kv_block_list)
-        return self._list_cache[key]
+        return self._list_cache.get((kv_block_list,), None, lambda: kv_block_list_to_pairs(kv_block_list))
+
+    def _tiles(self, pairs: torch.Tensor, offsets: torch.Tensor, bs: int):
+        if bs >= 64 or not pairs.is_cuda or pairs.dtype != torch.int32 or offsets.dtype != torch.int32:
+            return None   # ops validates and reports what is wrong
+        # validated once per schedule (one synchronisation), then reused
+        return self._tile_cache.get((pairs, offsets), bs, lambda: ops.csr_to_tiles(pairs, offsets, bs).check())
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 pattern: PatternMetadata) -> torch.Tensor:
@@ -80,7 +116,8 @@ class HipBlockSparseBackend(AttentionBackend):
             raise NotImplementedError(
                 f"hip_block_sparse does not run pattern kind {pattern.kind!r} (data-dependent top-k "
                 "selection is not a block schedule)")
-        out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs)
+        tiles = self._tiles(pairs, offsets, bs) if q.size(2) > 1 else None
+        out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs, tiles=tiles)
         self.last_kernel = "decode" if q.size(2) == 1 else "prefill"
         self._last_actual_backend = "hip_block_sparse"
         return out

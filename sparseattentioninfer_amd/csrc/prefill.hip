@@ -63,6 +63,12 @@ struct PrefillArgs {
   int64_t pairs_stride;
   const int32_t* offsets;
   int64_t offsets_stride;
+  // Tile schedules of finer blocks (16 or 32): pairs hold 64-key tiles of 64-row query tiles,
+  // tile_masks[r * masks_stride + e] the retained sub-blocks of entry e (bit sr * (64 / b) + sc
+  // for query sub-block sr, key sub-block sc); sub_log2 = log2(b), 0 without masks.
+  const int32_t* tile_masks;
+  int64_t masks_stride;
+  int sub_log2;
   int R;             // CSR rows
   int heads_per_row; // query heads that read one CSR row
   int head_splits;   // heads_per_row / heads per workgroup
@@ -114,7 +120,9 @@ __device__ __forceinline__ void load_lds16(const void* vaddr, uint32_t lds) {
 // Waits for the calling wave's direct loads (and any other vector memory access).
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
-template <bool BF16, int D, int HW>
+// SUB: tile schedules with sub-block masks (block sizes 16 and 32); without it the mask
+// bookkeeping compiles away.
+template <bool BF16, int D, int HW, bool SUB>
 struct Prefill {
   using E = Elem<BF16>;
   static constexpr int NW = 2 * HW;              // waves: HW query heads x two 32-row halves
@@ -252,6 +260,7 @@ struct Prefill {
     const elem_t* kb;
     const elem_t* vb;
     const int32_t* prow;
+    const int32_t* mrow;  // tile masks of the row (sub-block schedules)
     int e0, n_tiles, tpb_mask;
     bool cached;
     int q_row0, q_abs_tile_max, q_abs_min;
@@ -261,7 +270,8 @@ struct Prefill {
   // split hs.  Each wave owns 32 rows (half hf) of one query head; every K/V tile staged in
   // LDS feeds all NW waves.  Caches the CSR row of the query tile in s_row (callers barrier
   // before, so no wave still reads it).
-  static __device__ __forceinline__ Item setup(const PrefillArgs& a, int qt, int r, int hs, int b, int32_t* s_row) {
+  static __device__ __forceinline__ Item setup(const PrefillArgs& a, int qt, int r, int hs, int b, int32_t* s_row,
+                                               int32_t* s_mask) {
     Item it;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -280,11 +290,15 @@ struct Prefill {
     const int qblk = qt >> a.qpb_log2;
     const int32_t* offs = a.offsets + r * a.offsets_stride;
     it.prow = a.pairs + r * a.pairs_stride;
+    it.mrow = SUB ? a.tile_masks + r * a.masks_stride : nullptr;
     it.e0 = offs[qblk];
     const int n_ent = offs[qblk + 1] - it.e0;
     it.cached = n_ent <= ROW_CACHE;
-    if (it.cached)
+    if (it.cached) {
       for (int x = tid; x < n_ent; x += NT) s_row[x] = it.prow[it.e0 + x];
+      if (SUB)
+        for (int x = tid; x < n_ent; x += NT) s_mask[x] = it.mrow[it.e0 + x];
+    }
     it.n_tiles = n_ent << a.tpb_log2;
     it.tpb_mask = (1 << a.tpb_log2) - 1;
     const int q_tile0 = qt * QTILE;
@@ -308,6 +322,36 @@ struct Prefill {
     const int blk = it.cached ? s_row[e]
                               : __hip_atomic_load(it.prow + it.e0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return (blk << a.tpb_log2) + (t & it.tpb_mask);
+  }
+
+  static __device__ __forceinline__ int sub_log2(const PrefillArgs& a) { return SUB ? a.sub_log2 : 0; }
+
+  // Sub-block mask of schedule position t (tile schedules only; t indexes entries there).
+  static __device__ __forceinline__ uint32_t mask_of(const Item& it, const int32_t* s_mask, int t) {
+    return (uint32_t)(it.cached ? s_mask[t]
+                                : __hip_atomic_load(it.mrow + it.e0 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  }
+
+  // Whether a sub-block mask drops any sub-block of its tile.
+  static __device__ __forceinline__ bool partial_mask(const PrefillArgs& a, uint32_t m) {
+    if (!sub_log2(a)) return false;
+    const int s = 64 >> sub_log2(a);
+    return m != (s == 4 ? 0xffffu : 0xfu);
+  }
+
+  // Key sub-blocks of the tile visible to this lane's query row (local row hf*32 + l32 of
+  // the 64-row query tile) under sub-block mask m: bit sc for key sub-block sc; all ones
+  // without sub-blocks.
+  static __device__ __forceinline__ uint32_t row_bits(const PrefillArgs& a, uint32_t m, int hf, int l32) {
+    return sub_log2(a) ? m >> (((hf * QT + l32) >> sub_log2(a)) * (64 >> sub_log2(a))) : 0xffffffffu;
+  }
+
+  // This lane's key limit in 32-key half j, 16-key chunk h of a tile: lim (the last visible
+  // key offset minus 8g), or -1 (nothing visible) where the row's bits drop the sub-block
+  // of that chunk.  A 16-key chunk never straddles sub-blocks (b >= 16).
+  static __device__ __forceinline__ int chunk_lim(const PrefillArgs& a, uint32_t bits, int lim, int j, int h) {
+    const int sh = sub_log2(a) ? (32 * j + 16 * h) >> sub_log2(a) : 0;
+    return ((bits >> sh) & 1u) ? lim : -1;
   }
 
   // First tile at or after t that can contribute: tiles entirely past T_k or above the
@@ -360,13 +404,18 @@ struct Prefill {
   // Online softmax over the 32-key half j of the current tile for this wave's 32 rows.
   // Scores are raw; p = 2^(s*c - m_ref).  Returns the P^T operands of the two 16-key chunks.
   template <bool MASK>
-  static __device__ __forceinline__ void softmax_half(f32x16& S, u32x4 (&P)[2], f32x16 (&O)[D / 32],
-                                                      float& m_ref, float& l_run, float c, int lim, int j) {
+  static __device__ __forceinline__ void softmax_half(const PrefillArgs& a, f32x16& S, u32x4 (&P)[2],
+                                                      f32x16 (&O)[D / 32], float& m_ref, float& l_run, float c,
+                                                      uint32_t bits, int lim, int j) {
     if (MASK) {
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr) {
-        const int key = 32 * j + 16 * (rr >> 3) + (rr & 7);  // minus 8g, folded into lim
-        if (key > lim) S[rr] = -__builtin_inff();
+      for (int h = 0; h < 2; ++h) {
+        const int lh = chunk_lim(a, bits, lim, j, h);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = 32 * j + 16 * h + e;  // minus 8g, folded into the limit
+          if (key > lh) S[8 * h + e] = -__builtin_inff();
+        }
       }
     }
     float mx = S[0];
@@ -402,9 +451,9 @@ struct Prefill {
   // One 64-key tile: S^T = K Q^T per 32-key half, softmax, O^T += V^T P^T.  The softmax of
   // one half can run under the matrix instructions of the other half.
   template <bool MASK>
-  static __device__ __forceinline__ void tile(const char* cK, const char* cV, const Frag& f,
+  static __device__ __forceinline__ void tile(const PrefillArgs& a, const char* cK, const char* cV, const Frag& f,
                                               const u32x4 (&qf)[D / 16], f32x16 (&O)[D / 32], float& m_ref,
-                                              float& l_run, float c, int lim) {
+                                              float& l_run, float c, uint32_t bits, int lim) {
     // The two key halves are independent accumulation chains; alternating them keeps the
     // matrix pipe busy while each MFMA waits for its predecessor's result.
     f32x16 S[2] = {f32x16{}, f32x16{}};
@@ -415,7 +464,7 @@ struct Prefill {
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       u32x4 P[2];
-      softmax_half<MASK>(S[j], P, O, m_ref, l_run, c, lim, j);
+      softmax_half<MASK>(a, S[j], P, O, m_ref, l_run, c, bits, lim, j);
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
@@ -426,12 +475,12 @@ struct Prefill {
   // One work item, one tile at a time: the next tile's direct loads run under the current
   // tile's compute (double buffer), or after it (single buffer).
   static __device__ __forceinline__ void item(const PrefillArgs& a, int qt, int r, int hs, int b, char* sKV,
-                                              int32_t* s_row) {
+                                              int32_t* s_row, int32_t* s_mask) {
     char* sK = sKV;
     char* sV = sKV + NBK * TILE_BYTES;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const Item it = setup(a, qt, r, hs, b, s_row);
+    const Item it = setup(a, qt, r, hs, b, s_row, s_mask);
     // Q^T as the B operand of S^T = K Q^T: lane holds row l32, d = 16c + 8g .. +7.
     u32x4 qf[D / 16];
     {
@@ -473,12 +522,14 @@ struct Prefill {
 
       // A wave whose 32 rows all precede the tile skips it (the other half may not).
       if (kt * KT <= it.q_abs_min + QT - 1) {
-        const bool need_mask = (kt * KT + KT - 1 > it.q_abs_min) || (kt * KT + KT > a.Tk);
+        const uint32_t m = sub_log2(a) ? mask_of(it, s_mask, t) : 0u;
+        const bool need_mask = (kt * KT + KT - 1 > it.q_abs_min) || (kt * KT + KT > a.Tk) || partial_mask(a, m);
         const int lim = min(it.q_abs_min + it.l32, a.Tk - 1) - kt * KT - 8 * it.g;
+        const uint32_t bits = row_bits(a, m, it.hf, it.l32);
         if (need_mask)
-          tile<true>(cK, cV, f, qf, O, m_ref, l_run, c, lim);
+          tile<true>(a, cK, cV, f, qf, O, m_ref, l_run, c, bits, lim);
         else
-          tile<false>(cK, cV, f, qf, O, m_ref, l_run, c, lim);
+          tile<false>(a, cK, cV, f, qf, O, m_ref, l_run, c, bits, lim);
       }
 
       if (NBK == 1 && tn < it.n_tiles) {
@@ -497,14 +548,24 @@ struct Prefill {
   }
 
   // ---- software-pipelined loop (four-head workgroups) ----------------------------------
-  // Masks (causal / past T_k, branch-free) one tile's S^T and returns its scaled row max.
-  // lim = last visible key offset in the tile minus 8g (past the tile when nothing is masked).
-  static __device__ __forceinline__ float mask_rowmax(f32x16 (&S)[2], int lim, float c) {
+  // Masks one tile's S^T (causal / past T_k / sub-blocks, branch-free): keys past the
+  // chunk limits of (bits, lim) become -inf.
+  static __device__ __forceinline__ void mask_tile(const PrefillArgs& a, f32x16 (&S)[2], uint32_t bits, int lim) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int rr = 0; rr < 16; ++rr)
-        S[j][rr] = (32 * j + 16 * (rr >> 3) + (rr & 7) > lim) ? -__builtin_inff() : S[j][rr];
+      for (int h = 0; h < 2; ++h) {
+        const int lh = chunk_lim(a, bits, lim, j, h);
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          S[j][8 * h + e] = (32 * j + 16 * h + e > lh) ? -__builtin_inff() : S[j][8 * h + e];
+      }
+  }
+
+  // Masks one tile's S^T (mask_tile) and returns its scaled row max.
+  static __device__ __forceinline__ float mask_rowmax(const PrefillArgs& a, f32x16 (&S)[2], uint32_t bits,
+                                                      int lim, float c) {
+    mask_tile(a, S, bits, lim);
     float mx = S[0][0];
 #pragma unroll
     for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, S[0][rr]);
@@ -538,12 +599,12 @@ struct Prefill {
   // V buffers).  Tiles that lie wholly after this wave's rows cost matrix work but add
   // p == 0.
   static __device__ __forceinline__ void item_pipelined(const PrefillArgs& a, int qt, int r, int hs, int b,
-                                                        char* sKV, char* sQ, int32_t* s_row) {
+                                                        char* sKV, char* sQ, int32_t* s_row, int32_t* s_mask) {
     char* sK = sKV;
     char* sV = sKV + NBK * TILE_BYTES;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const Item it = setup(a, qt, r, hs, b, s_row);
+    const Item it = setup(a, qt, r, hs, b, s_row, s_mask);
     const char* sQw = sQ + wave * WAVE_BYTES;
     {  // Q^T operand of this wave into LDS, in fragment order
       const elem_t* qs = q_src(a, it);
@@ -570,6 +631,8 @@ struct Prefill {
     int t_nxt = t_cur < n_tiles ? next_usable(a, it, s_row, t_cur + 1) : n_tiles;
     int kt_cur = t_cur < n_tiles ? tile_of(a, it, s_row, t_cur) : 0;
     int kt_nxt = t_nxt < n_tiles ? tile_of(a, it, s_row, t_nxt) : 0;
+    const uint32_t m_cur = sub_log2(a) && t_cur < n_tiles ? mask_of(it, s_mask, t_cur) : 0u;
+    uint32_t m_nxt = sub_log2(a) && t_nxt < n_tiles ? mask_of(it, s_mask, t_nxt) : 0u;
     if (t_cur < n_tiles) {
       dma<true>(it.kb, a.k_st, dl.k, sK, kt_cur, a.Tk, wave, lane);
       dma<false>(it.vb, a.v_st, dl.v, sV, kt_cur, a.Tk, wave, lane);
@@ -586,7 +649,7 @@ struct Prefill {
 #pragma unroll
         for (int j = 0; j < 2; ++j) S[j] = E::mfma32(kfrag(sK, f, j, cc), qv, S[j]);
       }
-      mt_cur = mask_rowmax(S, lim0 - kt_cur * KT, c);
+      mt_cur = mask_rowmax(a, S, row_bits(a, m_cur, it.hf, it.l32), lim0 - kt_cur * KT, c);
     }
 
     int kb_cur = 0;  // K buffer of the current tile (tile t_nxt's is kb_cur + 1 mod 3)
@@ -597,6 +660,7 @@ struct Prefill {
       const int kb_nn = kb_nxt == 2 ? 0 : kb_nxt + 1;
       const int t_nn = t_nxt < n_tiles ? next_usable(a, it, s_row, t_nxt + 1) : n_tiles;
       const int kt_nn = t_nn < n_tiles ? tile_of(a, it, s_row, t_nn) : 0;
+      const uint32_t m_nn = sub_log2(a) && t_nn < n_tiles ? mask_of(it, s_mask, t_nn) : 0u;
       if (t_nn < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + kb_nn * TILE_BYTES, kt_nn, a.Tk, wave, lane);
       if (t_nxt < n_tiles) dma<false>(it.vb, a.v_st, dl.v, sV + (vb_cur ^ 1) * TILE_BYTES, kt_nxt, a.Tk, wave, lane);
       const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
@@ -654,13 +718,8 @@ struct Prefill {
       // Causal / T_k mask of the next tile, only where it cuts into the tile (uniform per
       // wave; about one tile in a row's window).
       const int kbase_n = kt_nxt * KT;
-      if (kbase_n + KT - 1 > it.q_abs_min || kbase_n + KT > a.Tk) {
-        const int lim = lim0 - kbase_n;
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int rr = 0; rr < 16; ++rr)
-            Sn[j][rr] = (32 * j + 16 * (rr >> 3) + (rr & 7) > lim) ? -__builtin_inff() : Sn[j][rr];
+      if (kbase_n + KT - 1 > it.q_abs_min || kbase_n + KT > a.Tk || partial_mask(a, m_nxt)) {
+        mask_tile(a, Sn, row_bits(a, m_nxt, it.hf, it.l32), lim0 - kbase_n);
       }
 
       // Block B: PV of this tile (D/8 MFMAs; V fragments read two MFMAs ahead) with the
@@ -696,6 +755,7 @@ struct Prefill {
       kt_cur = kt_nxt;
       t_nxt = t_nn;
       kt_nxt = kt_nn;
+      m_nxt = m_nn;
       kb_cur = kb_nxt;
       vb_cur ^= 1;
     }
@@ -715,19 +775,20 @@ struct Prefill {
   }
 
   static __device__ __forceinline__ void process(const PrefillArgs& a, int v, char* sKV, char* sQ,
-                                                 int32_t* s_row) {
+                                                 int32_t* s_row, int32_t* s_mask) {
     int qt, r, hs, b;
     decode_item(a, v, qt, r, hs, b);
     if constexpr (PIPE)
-      item_pipelined(a, qt, r, hs, b, sKV, sQ, s_row);
+      item_pipelined(a, qt, r, hs, b, sKV, sQ, s_row, s_mask);
     else
-      item(a, qt, r, hs, b, sKV, s_row);
+      item(a, qt, r, hs, b, sKV, s_row, s_mask);
   }
 
   static __device__ void run(const PrefillArgs& a) {
     __shared__ __attribute__((aligned(16))) char sKV[LDS_KV];
     __shared__ __attribute__((aligned(16))) char sQ[LDS_Q];
     __shared__ int32_t s_row[ROW_CACHE];
+    __shared__ int32_t s_mask[SUB ? ROW_CACHE : 1];  // sub-block masks of the cached row
     __shared__ int s_item;
     const int n_items = a.ntq * a.R * a.B * a.head_splits;
 
@@ -741,7 +802,7 @@ struct Prefill {
       const int xcd = blockIdx.x % N_XCD, seq = blockIdx.x / N_XCD;
       const int v = ((seq / chunk) * N_XCD + xcd) * chunk + seq % chunk;
       if (v >= n_items) return;  // padding workgroup of the last round
-      process(a, v, sKV, sQ, s_row);
+      process(a, v, sKV, sQ, s_row, s_mask);
       return;
     }
 
@@ -754,7 +815,7 @@ struct Prefill {
       const int v = s_item;
       __syncthreads();
       if (v >= n_items) break;
-      process(a, v, sKV, sQ, s_row);
+      process(a, v, sKV, sQ, s_row, s_mask);
     }
     if (threadIdx.x == 0 && atomicAdd(&a.counter[1], 1u) == gridDim.x - 1) {
       atomicExch(&a.counter[0], 0u);
@@ -764,21 +825,21 @@ struct Prefill {
 };
 
 // At most 256 registers per wave: two waves per SIMD (one 8-wave workgroup per CU).
-template <bool BF16, int D, int HW>
+template <bool BF16, int D, int HW, bool SUB>
 __global__ __launch_bounds__(128 * HW) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_kernel(PrefillArgs a) {
-  Prefill<BF16, D, HW>::run(a);
+  Prefill<BF16, D, HW, SUB>::run(a);
 }
 
 // Resident workgroups of one kernel instance per CU, and CUs, cached per device.
-template <bool BF16, int D, int HW>
+template <bool BF16, int D, int HW, bool SUB>
 static int resident_per_cu() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 1;
   if (!cached[dev]) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<BF16, D, HW>, 128 * HW, 0) != hipSuccess || n < 1)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_kernel<BF16, D, HW, SUB>, 128 * HW, 0) != hipSuccess || n < 1)
       n = 1;
     cached[dev] = n;
   }
@@ -797,12 +858,18 @@ static int num_cus() {
   return cached[dev];
 }
 
+template <bool BF16, int D, int HW, bool SUB>
+static hipError_t launch_sub(const PrefillArgs& a, int64_t n_items, int64_t item_grid, hipStream_t s) {
+  int64_t grid = item_grid;
+  if (a.counter) grid = std::min<int64_t>(n_items, (int64_t)num_cus() * resident_per_cu<BF16, D, HW, SUB>());
+  hipLaunchKernelGGL((prefill_kernel<BF16, D, HW, SUB>), dim3(grid), dim3(128 * HW), 0, s, a);
+  return hipGetLastError();
+}
+
 template <bool BF16, int D, int HW>
 static hipError_t launch_hw(const PrefillArgs& a, int64_t n_items, int64_t item_grid, hipStream_t s) {
-  int64_t grid = item_grid;
-  if (a.counter) grid = std::min<int64_t>(n_items, (int64_t)num_cus() * resident_per_cu<BF16, D, HW>());
-  hipLaunchKernelGGL((prefill_kernel<BF16, D, HW>), dim3(grid), dim3(128 * HW), 0, s, a);
-  return hipGetLastError();
+  return a.sub_log2 ? launch_sub<BF16, D, HW, true>(a, n_items, item_grid, s)
+                    : launch_sub<BF16, D, HW, false>(a, n_items, item_grid, s);
 }
 
 template <bool BF16, int D>
@@ -825,6 +892,7 @@ extern "C" int sa_prefill(int dtype,
                           void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
                           const int32_t* pairs, int64_t pairs_stride,
                           const int32_t* offsets, int64_t offsets_stride,
+                          const int32_t* tile_masks, int64_t tile_masks_stride,
                           int csr_rows, int nqb,
                           int B, int Hq, int Hkv, int T_q, int T_k, int D,
                           int block_size, int q_offset, float sm_scale,
@@ -840,13 +908,18 @@ extern "C" int sa_prefill(int dtype,
     return set_error(SA_E_SHAPE, "sa_prefill: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
   if (D != 64 && D != 128)
     return set_error(SA_E_HEADDIM, "sa_prefill: head dim %d not supported (64, 128)", D);
-  if (block_size != 64 && block_size != 128)
-    return set_error(SA_E_BLOCK, "sa_prefill: block size %d not supported (64, 128)", block_size);
+  if (block_size != 16 && block_size != 32 && block_size != 64 && block_size != 128)
+    return set_error(SA_E_BLOCK, "sa_prefill: block size %d not supported (16, 32, 64, 128)", block_size);
+  const bool tiled = block_size < 64;  // schedule of 64 x 64 tiles with sub-block masks
+  if (tiled != (tile_masks != nullptr))
+    return set_error(SA_E_BLOCK, "sa_prefill: block size %d %s tile masks", block_size,
+                     tiled ? "needs" : "takes no");
   if (csr_rows != Hq && csr_rows != Hkv)
     return set_error(SA_E_CSR, "sa_prefill: csr_rows=%d must be Hq=%d or Hkv=%d", csr_rows, Hq, Hkv);
-  if (nqb != (int)ceil_div(T_q, block_size))
-    return set_error(SA_E_SHAPE, "sa_prefill: nqb=%d but ceil(T_q/block)=%lld", nqb,
-                     (long long)ceil_div(T_q, block_size));
+  const int row_block = tiled ? 64 : block_size;  // query rows per CSR query block
+  if (nqb != (int)ceil_div(T_q, row_block))
+    return set_error(SA_E_SHAPE, "sa_prefill: nqb=%d but ceil(T_q/%d)=%lld", nqb, row_block,
+                     (long long)ceil_div(T_q, row_block));
   if (B == 0 || T_q == 0) return 0;
   if (!q || !k || !v || !o || !pairs || !offsets)
     return set_error(SA_E_NULL, "sa_prefill: NULL tensor pointer");
@@ -870,6 +943,9 @@ extern "C" int sa_prefill(int dtype,
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_st = o_st;
   a.pairs = pairs; a.pairs_stride = pairs_stride;
   a.offsets = offsets; a.offsets_stride = offsets_stride;
+  a.tile_masks = tile_masks;
+  a.masks_stride = tile_masks_stride;
+  a.sub_log2 = block_size == 16 ? 4 : block_size == 32 ? 5 : 0;
   a.R = csr_rows;
   a.heads_per_row = Hq / csr_rows;
   const int hw = (a.heads_per_row % 4 == 0) ? 4 : (a.heads_per_row % 2 == 0) ? 2 : 1;

@@ -46,6 +46,69 @@ def _prefill_workspace(t: torch.Tensor) -> torch.Tensor:
     return ws
 
 
+class TileSchedule:
+    """A CSR schedule of block size 16 or 32 regrouped into 64 x 64 tiles (``csr_to_tiles``).
+
+    ``pairs`` / ``masks [R, width]`` and ``offsets [R, ceil(NQB / s) + 1]``
+    int32 on the GPU (s = 64 / block_size); ``status`` is a device int that
+    stays 0 for a well-formed input CSR (bit 0: width overflow, bit 1: a query
+    block's ids not ascending).  :meth:`check` reads it (a synchronisation).
+    """
+
+    def __init__(self, pairs, masks, offsets, status, block_size):
+        self.pairs, self.masks, self.offsets, self.status = pairs, masks, offsets, status
+        self.block_size = block_size
+
+    def check(self) -> "TileSchedule":
+        st = int(self.status.item())
+        _require(not st & 1, "csr_to_tiles: a row needs more tiles than the CSR width (malformed offsets)")
+        _require(not st & 2, "csr_to_tiles: block ids of a query block are not ascending "
+                 "(the CSR holds sorted KB indices per query block)")
+        return self
+
+
+def csr_to_tiles(block_pairs: torch.Tensor, block_pair_offsets: torch.Tensor, block_size: int) -> TileSchedule:
+    """Regroups a block-16/32 CSR into the tile schedule of the prefill kernel (on the GPU).
+
+    One launch on the current stream, no synchronisation.  A row never needs
+    more tiles than it has entries, so the tile arrays take the input's width.
+    """
+    name = "csr_to_tiles"
+    _require(block_size in (16, 32), f"{name}: block_size {block_size} is not 16 or 32")
+    _require(block_pairs.is_cuda and block_pairs.dtype == torch.int32
+             and block_pair_offsets.dtype == torch.int32 and block_pair_offsets.device == block_pairs.device,
+             f"{name}: CSR tensors must be int32 on the GPU")
+    pairs = block_pairs.contiguous()
+    offsets = block_pair_offsets.contiguous()
+    R, nqb = pairs.size(0), offsets.size(1) - 1
+    nqt = -(-nqb // (64 // block_size))
+    width = max(1, pairs.size(1))
+    dev = pairs.device
+    tp = torch.empty(R, width, dtype=torch.int32, device=dev)
+    tm = torch.empty(R, width, dtype=torch.int32, device=dev)
+    to = torch.empty(R, nqt + 1, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    rc = _lib.load().sa_csr_to_tiles(
+        pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
+        R, nqb, block_size, tp.data_ptr(), tm.data_ptr(), tp.stride(0), width,
+        to.data_ptr(), to.stride(0), status.data_ptr(), _stream(pairs))
+    _lib.check("sa_csr_to_tiles", rc)
+    return TileSchedule(tp, tm, to, status, block_size)
+
+
+def _schedule_args(pairs, offsets, block_size, tiles: TileSchedule | None):
+    """Schedule arguments of sa_prefill: (pairs, offsets, masks) tensors to keep alive, the six
+    pointer/stride arguments, and the number of schedule query blocks."""
+    if block_size >= 64:
+        return pairs, offsets, None, [pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
+                                      None, 0], offsets.size(1) - 1
+    if tiles is None:
+        tiles = csr_to_tiles(pairs, offsets, block_size)
+    return tiles.pairs, tiles.offsets, tiles.masks, [
+        tiles.pairs.data_ptr(), tiles.pairs.stride(0), tiles.offsets.data_ptr(), tiles.offsets.stride(0),
+        tiles.masks.data_ptr(), tiles.masks.stride(0)], tiles.offsets.size(1) - 1
+
+
 def _require(cond: bool, msg: str) -> None:
     # The reference validates with `assert`; the same conditions raise AssertionError here,
     # but independent of Python's -O flag.
@@ -70,14 +133,17 @@ def _check_qkv(q, k, v, name):
 
 def universal_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           block_pairs: torch.Tensor, block_pair_offsets: torch.Tensor,
-                          block_size: int, *, q_offset: int | None = None) -> torch.Tensor:
+                          block_size: int, *, q_offset: int | None = None,
+                          tiles: TileSchedule | None = None) -> torch.Tensor:
     """Block-sparse causal attention over a CSR schedule; returns ``[B, Hq, T_q, D]``.
 
     ``q [B, Hq, T_q, D]``, ``k, v [B, Hkv, T_k, D]`` fp16/bf16 on the GPU;
     ``block_pairs [R, max_pairs]`` / ``block_pair_offsets [R, NQB+1]`` int32
     with ``R == Hq`` or ``R == Hkv``.  Query row ``t`` is at absolute position
     ``q_offset + t`` (default ``T_k - T_q``).  ``T_q == 1`` runs the decode
-    kernel (the reference runs its prefill kernel on one row).
+    kernel (the reference runs its prefill kernel on one row).  Block sizes 16
+    and 32 run the prefill kernel on 64 x 64 tiles with sub-block masks; pass
+    ``tiles = csr_to_tiles(...)`` to reuse one conversion across calls.
     """
     name = "universal_sparse_attn"
     _check_qkv(q, k, v, name)
@@ -117,18 +183,23 @@ def universal_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             1, None, 0, _stream(q))
         _lib.check("sa_decode", status)
         return out
-    _require(block_size in (64, 128), f"{name}: block_size {block_size} not supported by the "
-             "gfx950 prefill kernel (64, 128)")
+    _require(block_size <= 128, f"{name}: block_size {block_size} not supported by the "
+             "gfx950 prefill kernel (16, 32, 64, 128)")
+    _require(nqb == -(-T_q // block_size),
+             f"{name}: {nqb} CSR query blocks but T_q={T_q} needs {-(-T_q // block_size)}")
+    # `held` keeps the schedule tensors alive until the launch is enqueued: freed earlier,
+    # their memory could be handed to an allocation (the workspace below) ahead of the kernel.
+    *held, sched, nqb_k = _schedule_args(pairs, offsets, block_size, tiles)
     status = lib.sa_prefill(
         _DTYPES[q.dtype],
         q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
         k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
         v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
-        pairs.data_ptr(), pairs.stride(0),
-        offsets.data_ptr(), offsets.stride(0),
-        R, nqb, B, Hq, Hkv, T_q, T_k, D, block_size, int(q_offset), sm_scale,
+        *sched,
+        R, nqb_k, B, Hq, Hkv, T_q, T_k, D, block_size, int(q_offset), sm_scale,
         *_ws_args(_prefill_workspace(q)), _stream(q))
+    del held   # enqueued: a later reuse of this memory is ordered after the kernel on the stream
     _lib.check("sa_prefill", status)
     return out
 
@@ -232,17 +303,22 @@ class PreparedLaunch:
 
 
 def prepare_prefill(q, k, v, block_pairs, block_pair_offsets, block_size, *, out=None) -> PreparedLaunch:
-    """Validates like :func:`universal_sparse_attn` (T_q > 1) and binds the launch."""
+    """Validates like :func:`universal_sparse_attn` (T_q > 1) and binds the launch.
+
+    For block sizes 16 and 32 the tile schedule is converted once, here.
+    """
     name = "prepare_prefill"
     _check_qkv(q, k, v, name)
     B, Hq, T_q, D = q.shape
     Hkv, T_k = k.shape[1], k.shape[2]
-    _require(T_q > 1 and block_size in (64, 128), f"{name}: needs T_q > 1 and block 64/128")
+    _require(T_q > 1 and block_size in (16, 32, 64, 128), f"{name}: needs T_q > 1 and block 16/32/64/128")
     pairs = block_pairs.contiguous()
     offsets = block_pair_offsets.contiguous()
     _require(pairs.dtype == torch.int32 and offsets.dtype == torch.int32, f"{name}: CSR must be int32")
     R = pairs.size(0)
     _require(R in (Hq, Hkv) and offsets.size(0) == R, f"{name}: CSR rows {R} not Hq or Hkv")
+    _require(offsets.size(1) - 1 == -(-T_q // block_size), f"{name}: CSR query blocks do not cover T_q")
+    sp, so, sm, sched, nqb_k = _schedule_args(pairs, offsets, block_size, None)
     if out is None:
         out = torch.empty(B, Hq, T_q, D, dtype=q.dtype, device=q.device)
     args = [
@@ -251,10 +327,10 @@ def prepare_prefill(q, k, v, block_pairs, block_pair_offsets, block_size, *, out
         k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
         v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
         out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
-        pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
-        R, offsets.size(1) - 1, B, Hq, Hkv, T_q, T_k, D, block_size, T_k - T_q,
+        *sched,
+        R, nqb_k, B, Hq, Hkv, T_q, T_k, D, block_size, T_k - T_q,
         1.0 / math.sqrt(D), *_ws_args(_prefill_workspace(q)), _stream(q)]
-    return PreparedLaunch("sa_prefill", args, (q, k, v, pairs, offsets), out)
+    return PreparedLaunch("sa_prefill", args, (q, k, v, pairs, offsets, sp, so, sm), out)
 
 
 def prepare_paged_decode(q, k_pages, v_pages, block_table, kv_lens, sel, sel_off, *,

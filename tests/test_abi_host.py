@@ -28,7 +28,7 @@ def lib():
 
 def test_header_declares_entry_points():
     assert {"sa_abi_version", "sa_last_error", "sa_prefill", "sa_prefill_workspace_bytes", "sa_decode",
-            "sa_decode_workspace_bytes"} <= _declared()
+            "sa_decode_workspace_bytes", "sa_csr_to_tiles"} <= _declared()
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -46,8 +46,19 @@ def test_abi_version_and_error_string(lib):
 def test_argument_errors_are_reported_without_a_gpu(lib):
     # rejected before any HIP call: unsupported head dim
     st = lib.sa_prefill(0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
-                        None, 0, None, 0, 4, 1, 1, 4, 4, 64, 64, 96, 64, 0, 0.1, None, 0, None)
+                        None, 0, None, 0, None, 0, 4, 1, 1, 4, 4, 64, 64, 96, 64, 0, 0.1, None, 0, None)
     assert st == -3 and b"head dim 96" in lib.sa_last_error()
+    # block sizes 16 / 32 need a tile schedule (tile masks), 64 / 128 take none
+    st = lib.sa_prefill(0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
+                        None, 0, None, 0, None, 0, 4, 1, 1, 4, 4, 64, 64, 128, 16, 0, 0.1, None, 0, None)
+    assert st == -4 and b"needs tile masks" in lib.sa_last_error()
+    st = lib.sa_prefill(0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0, None, 0, 0, 0,
+                        None, 0, None, 0, 8, 1, 4, 1, 1, 4, 4, 64, 64, 128, 64, 0, 0.1, None, 0, None)
+    assert st == -4 and b"takes no tile masks" in lib.sa_last_error()
+    st = lib.sa_csr_to_tiles(None, 0, None, 0, 2, 4, 64, None, None, 0, 4, None, 0, None, None)
+    assert st == -4 and b"not 16 or 32" in lib.sa_last_error()
+    st = lib.sa_csr_to_tiles(None, 0, None, 0, 2, 4, 16, None, None, 0, 4, None, 0, None, None)
+    assert st == -6
     st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, None, 0, None, 0, 0, None, 0, 0,
                        3, None, 0, 0, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
     assert st == -5 and b"sel_rows=3" in lib.sa_last_error()

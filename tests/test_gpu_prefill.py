@@ -169,7 +169,7 @@ def test_persistent_and_grid_launches_agree_and_reset_workspace():
         o = torch.empty_like(q)
         st = lib.sa_prefill(0, q.data_ptr(), *q.stride()[:3], k.data_ptr(), *k.stride()[:3],
                             v.data_ptr(), *v.stride()[:3], o.data_ptr(), *o.stride()[:3],
-                            pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
+                            pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0), None, 0,
                             Hkv, offsets.size(1) - 1, B, Hq, Hkv, T, T, D, bs, 0, 1.0 / math.sqrt(D),
                             w.data_ptr() if w is not None else None, 8 if w is not None else 0,
                             torch.cuda.current_stream().cuda_stream)
