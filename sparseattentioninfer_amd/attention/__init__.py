@@ -24,9 +24,15 @@ def get_backend(name: str, **kwargs) -> AttentionBackend:
     return _REGISTRY[name](**kwargs)
 
 
+def register_backend(name: str, cls: type[AttentionBackend]) -> None:
+    """Adds a backend class under ``name`` (callers then select it with :func:`get_backend`)."""
+    _REGISTRY[name] = cls
+
+
 def register_into(registry: dict) -> None:
     """Adds this backend to another registry dict (e.g. the reference's ``_REGISTRY``)."""
     registry[BACKEND_NAME] = HipBlockSparseBackend
 
 
-__all__ = ["AttentionBackend", "HipBlockSparseBackend", "get_backend", "register_into", "BACKEND_NAME"]
+__all__ = ["AttentionBackend", "HipBlockSparseBackend", "get_backend", "register_backend", "register_into",
+           "BACKEND_NAME"]

@@ -64,6 +64,8 @@ class _DerivedCache:
 class HipBlockSparseBackend(AttentionBackend):
     """Block-sparse attention on hand-written HIP kernels for gfx950."""
 
+    supports_gqa = True   # k/v may carry H_kv < H heads; callers need not repeat them
+
     def __init__(self):
         self._last_actual_backend = "unknown"
         self.last_kernel = None          # "prefill" or "decode" after a forward
@@ -76,15 +78,25 @@ class HipBlockSparseBackend(AttentionBackend):
         return self._last_actual_backend
 
     def _dense_schedule(self, T_q: int, T_k: int, rows: int, device) -> tuple:
-        key = (T_q, T_k, rows, str(device))
-        if key not in self._dense_cache:
-            bs = _DENSE_BLOCK
-            nqb, nkb = -(-T_q // bs), -(-T_k // bs)
-            qa = (T_k - T_q) // bs + torch.arange(nqb)
+        """Full causal schedule: query block qb keeps key blocks 0 .. the block of its last
+        row's absolute position (``T_k - T_q`` need not be a multiple of the block).  It
+        depends on the shape only through those limits, so decode steps inside one KV block
+        share it."""
+        bs = _DENSE_BLOCK
+        nqb, nkb = -(-T_q // bs), -(-T_k // bs)
+        off = T_k - T_q
+        last = tuple(min((off + min((qb + 1) * bs, T_q) - 1) // bs, nkb - 1) for qb in range(nqb))
+        key = (nkb, last, rows, str(device))
+        hit = self._dense_cache.get(key)
+        if hit is None:
+            qa = torch.tensor(last, dtype=torch.long)
             bm = (torch.arange(nkb)[None, :] <= qa[:, None])[None].expand(rows, nqb, nkb)
             pairs, offsets = block_mask_to_csr(bm.contiguous())
-            self._dense_cache[key] = (pairs.to(device), offsets.to(device), bs)
-        return self._dense_cache[key]
+            hit = (pairs.to(device), offsets.to(device), bs)
+            self._dense_cache[key] = hit
+            if len(self._dense_cache) > _DERIVED_CACHE_SIZE:
+                self._dense_cache.pop(next(iter(self._dense_cache)))
+        return hit
 
     def _list_schedule(self, kv_block_list: torch.Tensor) -> tuple:
         return self._list_cache.get((kv_block_list,), None, lambda: kv_block_list_to_pairs(kv_block_list))
@@ -95,14 +107,10 @@ class HipBlockSparseBackend(AttentionBackend):
         # validated once per schedule (one synchronisation), then reused
         return self._tile_cache.get((pairs, offsets), bs, lambda: ops.csr_to_tiles(pairs, offsets, bs).check())
 
-    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                pattern: PatternMetadata) -> torch.Tensor:
-        if not q.is_cuda:
-            raise RuntimeError("hip_block_sparse runs on ROCm GPU tensors only; got a CPU tensor "
-                               "(this backend has no CPU fallback)")
+    def _schedule(self, T_q: int, T_k: int, kv_heads: int, device, pattern: PatternMetadata) -> tuple:
         if pattern.kind == "dense":
-            pairs, offsets, bs = self._dense_schedule(q.size(2), k.size(2), k.size(1), q.device)
-        elif pattern.kind in ("mask", "local"):
+            return self._dense_schedule(T_q, T_k, kv_heads, device)
+        if pattern.kind in ("mask", "local"):
             bs = pattern.block_size
             if bs is None:
                 raise ValueError("hip_block_sparse needs a block-sparse schedule; pattern.block_size is None")
@@ -112,12 +120,44 @@ class HipBlockSparseBackend(AttentionBackend):
                 pairs, offsets = self._list_schedule(pattern.kv_block_list)
             else:
                 raise ValueError("hip_block_sparse needs block_pairs/block_pair_offsets or kv_block_list")
-        else:
-            raise NotImplementedError(
-                f"hip_block_sparse does not run pattern kind {pattern.kind!r} (data-dependent top-k "
-                "selection is not a block schedule)")
+            return pairs, offsets, bs
+        raise NotImplementedError(
+            f"hip_block_sparse does not run pattern kind {pattern.kind!r} (data-dependent top-k "
+            "selection is not a block schedule)")
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                pattern: PatternMetadata) -> torch.Tensor:
+        if not q.is_cuda:
+            raise RuntimeError("hip_block_sparse runs on ROCm GPU tensors only; got a CPU tensor "
+                               "(this backend has no CPU fallback)")
+        pairs, offsets, bs = self._schedule(q.size(2), k.size(2), k.size(1), q.device, pattern)
         tiles = self._tiles(pairs, offsets, bs) if q.size(2) > 1 else None
         out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs, tiles=tiles)
         self.last_kernel = "decode" if q.size(2) == 1 else "prefill"
+        self._last_actual_backend = "hip_block_sparse"
+        return out
+
+    def forward_paged(self, q: torch.Tensor, store, pattern: PatternMetadata) -> torch.Tensor:
+        """One decode token per sequence (``q [B, H, 1, D]``) against a paged store.
+
+        ``store`` is a :class:`~sparseattentioninfer_amd.models.kv_cache.PagedKVStore` already
+        holding the new token; the pattern's single CSR query block (the row of the last
+        position) is shared by the batch, and its block size must equal the page size.
+        """
+        if not q.is_cuda:
+            raise RuntimeError("hip_block_sparse runs on ROCm GPU tensors only")
+        if q.size(2) != 1:
+            raise ValueError(f"forward_paged decodes one token per sequence; got T_q={q.size(2)}")
+        pairs, offsets, bs = self._schedule(1, store.seq_len(), store.heads, q.device, pattern)
+        if bs != store.page:
+            raise ValueError(f"schedule block {bs} differs from the cache page {store.page}")
+        if offsets.size(1) != 2:
+            raise ValueError(f"decode expects one CSR query block, got {offsets.size(1) - 1}")
+        B, R = q.size(0), pairs.size(0)
+        sel = pairs.contiguous()[None].expand(B, R, pairs.size(1))
+        sel_off = offsets.contiguous()[None].expand(B, R, 2)
+        out = ops.paged_sparse_decode(q, store.k_pages, store.v_pages, store.block_table, store.kv_lens,
+                                      sel, sel_off, num_splits=0)
+        self.last_kernel = "decode"
         self._last_actual_backend = "hip_block_sparse"
         return out

@@ -225,6 +225,14 @@ def decode_workspace_bytes(B: int, Hq: int, D: int, num_splits: int) -> int:
     return int(_lib.load().sa_decode_workspace_bytes(B, Hq, D, num_splits))
 
 
+def auto_decode_splits(B: int, rows: int, max_sel: int, target_workgroups: int = 512) -> int:
+    """Splits of each (sequence, row) block list so that a decode launch has about
+    ``target_workgroups`` workgroups (two per CU), keeping at least two blocks per split."""
+    base = max(1, B * rows)
+    want = -(-target_workgroups // base)
+    return max(1, min(want, max_sel // 2, 16))
+
+
 def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
                         block_table: torch.Tensor, kv_lens: torch.Tensor,
                         sel: torch.Tensor, sel_off: torch.Tensor, *,
@@ -237,7 +245,8 @@ def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.T
     -> page); ``kv_lens [B]`` int32; ``sel [B, R, max_sel]`` / ``sel_off
     [B, R, 2]`` int32 retained logical blocks per (sequence, row), R = Hq or
     Hkv.  ``num_splits > 1`` splits each row over workgroups and needs a
-    byte workspace of :func:`decode_workspace_bytes` (allocated if omitted).
+    byte workspace of :func:`decode_workspace_bytes` (allocated if omitted);
+    ``num_splits=0`` picks the count with :func:`auto_decode_splits`.
     """
     name = "paged_sparse_decode"
     q3 = q.reshape(q.shape[0], q.shape[1], q.shape[-1]) if q.dim() == 4 else q
@@ -255,6 +264,8 @@ def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.T
     _require(R in (Hq, Hkv) and sel_off.shape[:2] == (B, R) and sel.shape[0] == B, f"{name}: bad sel rows")
     _require(sel.stride(2) == 1 and block_table.stride(1) == 1 and kv_lens.is_contiguous()
              and sel_off.stride(2) == 1, f"{name}: index tensors must be contiguous in the last dim")
+    if num_splits == 0:
+        num_splits = auto_decode_splits(B, R, sel.shape[2])
     if out is None:
         out = torch.empty(B, Hq, D, dtype=q3.dtype, device=q3.device)
     lib = _lib.load()

@@ -12,9 +12,11 @@ Rows here are CSR rows: one per KV group when the pattern is group-shared.
 """
 from __future__ import annotations
 
+from collections import OrderedDict
+
 import torch
 
-from .base import PatternMetadata, SparsePattern, block_mask_to_csr, causal_block_keep_ratio
+from .base import PatternMetadata, SparsePattern, block_mask_to_csr
 
 
 def _causal_limit(nqb: int, nkb: int, q_block_offset: int) -> torch.Tensor:
@@ -86,29 +88,44 @@ def bernoulli_block_mask(rows: int, nqb: int, nkb: int, *, density: float, seed:
 
 
 class _BlockMaskPattern(SparsePattern):
-    """Shared plumbing: block mask -> PatternMetadata, cached per shape and device."""
+    """Shared plumbing: block mask -> PatternMetadata.
+
+    The CSR depends on the shape only through the block counts (nqb, nkb) and
+    the query block offset, so decode steps inside one KV block reuse it; the
+    device copies live in a small LRU keyed that way.  The keep ratio is
+    computed from host-side counts, so ``build`` never waits for the GPU.
+    """
+
+    CACHE_SIZE = 32
 
     def __init__(self, block_size: int, rows: int):
         self.block_size = int(block_size)
         self.rows = int(rows)
-        self._cache: dict = {}
+        self._cache: OrderedDict = OrderedDict()
 
     def _block_mask(self, nqb: int, nkb: int, q_block_offset: int) -> torch.Tensor:
         raise NotImplementedError
 
     def build(self, q: torch.Tensor, k: torch.Tensor, causal: bool = True) -> PatternMetadata:
         T_q, T_k = q.size(2), k.size(2)
-        key = (T_q, T_k, str(q.device))
-        if key not in self._cache:
-            bs = self.block_size
-            nqb, nkb = -(-T_q // bs), -(-T_k // bs)
-            bm = self._block_mask(nqb, nkb, max(0, T_k - T_q) // bs)
-            pairs, offsets = block_mask_to_csr(bm)
-            pairs, offsets = pairs.to(q.device), offsets.to(q.device)
-            kr = causal_block_keep_ratio(offsets, T_q, T_k, bs)
-            self._cache[key] = PatternMetadata(kind="mask", keep_ratio=kr, block_size=bs,
-                                               block_pairs=pairs, block_pair_offsets=offsets)
-        return self._cache[key]
+        bs = self.block_size
+        nqb, nkb, qbo = -(-T_q // bs), -(-T_k // bs), max(0, T_k - T_q) // bs
+        key = (nqb, nkb, qbo, str(q.device))
+        entry = self._cache.get(key)
+        if entry is None:
+            pairs, offsets = block_mask_to_csr(self._block_mask(nqb, nkb, qbo))
+            kept = int(offsets[:, -1].long().sum())
+            entry = (pairs.to(q.device), offsets.to(q.device), kept)
+            self._cache[key] = entry
+            if len(self._cache) > self.CACHE_SIZE:
+                self._cache.popitem(last=False)
+        else:
+            self._cache.move_to_end(key)
+        pairs, offsets, kept = entry
+        denom = sum(min(qbo + i + 1, nkb) for i in range(nqb)) * self.rows
+        kr = min(1.0, kept / denom) if denom > 0 else 0.0
+        return PatternMetadata(kind="mask", keep_ratio=kr, block_size=bs,
+                               block_pairs=pairs, block_pair_offsets=offsets)
 
 
 class SeededBigBirdPattern(_BlockMaskPattern):
