@@ -13,6 +13,12 @@ sequences, 16384 cached tokens each in 64-token pages, 14 retained blocks per
 dense-masked PyTorch path (the reference's ``MaskedSdpaBackend`` arithmetic,
 restated in ``oracle/``) on the host cores, on a bounded sample of configs[2].
 
+``e2e`` (skip with ``--no-e2e``) is configs[4]: a random-init Qwen3-4B-architecture decoder (36
+layers, BigBird window 3 / global 2 / random 3 in layers 0-17, dense causal
+in 18-35, both on the HIP kernels) generating greedily from an 8192-token
+prompt for 8 sequences, reporting TTFT and decode tokens/s with the KV cache
+in pages.
+
 Inputs are synthetic (seeded N(0,1)) and resident in HBM before timing.
 ``--gpus`` above 1 is refused: this build measures one GPU.
 """
@@ -48,6 +54,10 @@ def parse():
     ap.add_argument("--decode-splits", type=int, default=0, help="0 = time 1 and 2, keep the faster")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end Qwen3 workload (configs[4])")
+    ap.add_argument("--e2e-batch", type=int, default=8)
+    ap.add_argument("--e2e-prompt", type=int, default=8192)
+    ap.add_argument("--e2e-steps", type=int, default=256)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a 1 GiB device copy (for scaling FETCH_SIZE / WRITE_SIZE counters)")
     return ap.parse_args()
@@ -208,6 +218,30 @@ def cpu_baseline(prefill_res, budget_s):
                        f"time; host os.cpu_count()={os.cpu_count()}, affinity={aff}")}
 
 
+def run_e2e(args, dev):
+    """TTFT and decode tokens/s of greedy generation (one warm-up generation first)."""
+    import torch
+    from sparseattentioninfer_amd.qwen3.runtime import build_model, greedy_generate, qwen3_config
+    cfg = qwen3_config(sparse_layers=range(18), pattern="seeded_bigbird", block_size=BS, window=3,
+                       global_blocks=2, random_blocks=3, seed=11)
+    t0 = time.perf_counter()
+    model = build_model(cfg, device=dev, dtype=torch.bfloat16, seed=0)
+    build_s = time.perf_counter() - t0
+    B, T, steps = args.e2e_batch, args.e2e_prompt, args.e2e_steps
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(12)).to(dev)
+    greedy_generate(model, ids, min(steps, 8), cache="paged")          # warm-up (libraries, schedules)
+    torch.cuda.synchronize()
+    g = greedy_generate(model, ids, steps, cache="paged", shuffle_seed=13)
+    kv_bytes = sum(layer.store.k_pages.numel() * 2 * 2 for layer in g["cache"].layers)
+    times = sorted(g["decode_step_times_s"])
+    return {"workload": f"configs[4]: Qwen3-4B-arch random-init, B={B}, prompt {T}, {steps} greedy steps, "
+                        "BigBird (3,2,3) block 64 in layers 0-17, dense causal 18-35, paged KV cache",
+            "ttft_s": g["ttft_s"], "decode_tok_per_s": g["decode_tokens_per_s"],
+            "decode_ms_per_step_median": 1e3 * times[len(times) // 2],
+            "decode_ms_per_step_mean": 1e3 * g["decode_total_s"] / max(1, steps),
+            "kv_cache_gb": kv_bytes / 1e9, "model_build_s": build_s}
+
+
 def copy_calibration(dev):
     import torch
     n = 1 << 30
@@ -253,6 +287,13 @@ def main():
         if pre is None:
             line.update(value=round(dec["tok_per_s"], 1), unit="tok/s", ms_per_step=round(dec["us_per_step"] / 1e3, 4),
                         config={"workload": dec["workload"]}, roofline=line["decode"]["roofline"])
+    if not args.no_e2e and args.only == "all":
+        try:
+            e2e = run_e2e(args, dev)
+            line["e2e"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in e2e.items()}
+        except Exception as exc:   # the kernel figures above stay valid; say what failed
+            line["e2e"] = {"error": f"{type(exc).__name__}: {exc}"}
+            print(f"e2e leg failed: {exc!r}", file=sys.stderr)
     if pre is not None and not args.no_cpu_baseline:
         cb = cpu_baseline(pre, args.cpu_seconds)
         cb["value"] = round(cb["value"], 5)
