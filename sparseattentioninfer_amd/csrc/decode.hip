@@ -42,7 +42,25 @@ struct DecodeArgs {
 };
 
 constexpr int DEC_WAVES = 4;
-constexpr int DEC_NI = 8;  // 16-byte loads of K (and of V) per lane per round
+constexpr int DEC_NI = 8;        // 16-byte loads of K (and of V) per lane per round
+constexpr int DEC_CACHE = 512;   // retained blocks of a workgroup staged in LDS (longer lists read HBM)
+
+// x as held by the lane that DPP control CTRL selects (quad permutes, row mirrors: within 16 lanes).
+template <int CTRL>
+__device__ __forceinline__ float dpp_get(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the LPR (8 or 16) consecutive lanes of one key row; every lane of the row receives it.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float x) {
+  static_assert(LPR == 8 || LPR == 16, "key rows span 8 or 16 lanes");
+  x += dpp_get<0xB1>(x);   // quad_perm [1,0,3,2]: lane pairs
+  x += dpp_get<0x4E>(x);   // quad_perm [2,3,0,1]: quads
+  x += dpp_get<0x141>(x);  // row_half_mirror (lane i <-> 7 - i): the two quads of 8 lanes
+  if constexpr (LPR == 16) x += dpp_get<0x140>(x);  // row_mirror (lane i <-> 15 - i): the two halves
+  return x;
+}
 
 template <bool BF16, int D, int NH>
 struct Decode {
@@ -51,24 +69,125 @@ struct Decode {
   static constexpr int KPI = 64 / LPR;     // key rows per load instruction
   static constexpr int CH = DEC_NI * KPI;  // keys per round
 
-  static __device__ __forceinline__ void unpack8(u32x4 w, float* f) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = E::to_f32(static_cast<elem_t>(w[i] & 0xffffu));
-      f[2 * i + 1] = E::to_f32(static_cast<elem_t>(w[i] >> 16));
+  // One round of a wave: DEC_NI key rows of K and of V per lane, and the valid key count.
+  struct Round {
+    u32x4 k[DEC_NI], v[DEC_NI];
+    int nk;
+  };
+
+  struct Ctx {
+    const int32_t* s_blk;  // staged logical blocks (when cached)
+    const int32_t* s_pg;   // staged pages (paged caches)
+    const int32_t* selp;   // the global list (when not cached)
+    int lo, b, kvh, L, rpb, kg, dc;
+    bool cached;
+  };
+
+  // Loads round `it` of the workgroup's list: keys k0 .. k0 + CH - 1 of retained entry it / rpb.
+  // Blocks past kv_len or with negative ids load nothing (nk = 0).
+  static __device__ __forceinline__ void issue(const DecodeArgs& a, const Ctx& c, int it, Round& R) {
+    const int x = it / c.rpb;
+    const int k0 = (it - x * c.rpb) * CH;
+    int lb, pg = 0;
+    if (c.cached) {
+      lb = c.s_blk[x];
+      pg = c.s_pg[x];
+    } else {
+      lb = c.selp[c.lo + x];
+      if (a.block_table && lb >= 0 && (int64_t)lb * a.page < c.L) pg = a.block_table[c.b * a.bt_stride + lb];
     }
+    lb = __builtin_amdgcn_readfirstlane(lb);
+    pg = __builtin_amdgcn_readfirstlane(pg);
+    const int nk = lb < 0 ? 0 : max(0, min(min(CH, a.page - k0), c.L - lb * a.page - k0));
+    R.nk = nk;
+    const elem_t* kb;
+    const elem_t* vb;
+    if (a.block_table) {
+      const int64_t base = (int64_t)pg * a.kv_sb + c.kvh * a.kv_sh + (int64_t)k0 * a.kv_st;
+      kb = a.k + base;
+      vb = a.v + base;
+    } else {
+      const int64_t base = c.b * a.kv_sb + c.kvh * a.kv_sh + ((int64_t)lb * a.page + k0) * a.kv_st;
+      kb = a.k + base;
+      vb = a.v + base;
+    }
+#pragma unroll
+    for (int i = 0; i < DEC_NI; ++i) {
+      const int key = c.kg + KPI * i;
+      const bool ok = key < nk;
+      R.k[i] = ok ? *reinterpret_cast<const u32x4*>(kb + key * a.kv_st + c.dc * 8) : u32x4{0, 0, 0, 0};
+      R.v[i] = ok ? *reinterpret_cast<const u32x4*>(vb + key * a.kv_st + c.dc * 8) : u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // Online softmax over one round for the NH heads: scores by packed dot products, summed over
+  // the LPR lanes of each key row; P rounded to the element type, PV by packed dot products over
+  // key pairs.
+  static __device__ __forceinline__ void compute(const Round& R, const uint32_t (&qp)[NH][4], float scale,
+                                                 int kg, float (&m_run)[NH], float (&l_run)[NH],
+                                                 float (&acc)[NH][8]) {
+    float sc[DEC_NI][NH];
+#pragma unroll
+    for (int i = 0; i < DEC_NI; ++i)
+#pragma unroll
+      for (int h = 0; h < NH; ++h) {
+        float p = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) p = E::dot2(qp[h][w], R.k[i][w], p);
+        sc[i][h] = row_sum<LPR>(p);
+      }
+    uint32_t pp[NH][DEC_NI / 2];
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int i = 0; i < DEC_NI; ++i) {
+        const float x = (kg + KPI * i < R.nk) ? sc[i][h] * scale : -__builtin_inff();
+        sc[i][h] = x;
+        mx = fmaxf(mx, x);
+      }
+#pragma unroll
+      for (int msk = LPR; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+      const float m_new = fmaxf(m_run[h], mx);
+      const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+      const float alpha = fast_exp2(m_run[h] - m_use);
+      m_run[h] = m_new;
+      l_run[h] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
+#pragma unroll
+      for (int j = 0; j < DEC_NI / 2; ++j) {
+        const float p0 = fast_exp2(sc[2 * j][h] - m_use);
+        const float p1 = fast_exp2(sc[2 * j + 1][h] - m_use);
+        l_run[h] += p0 + p1;
+        pp[h][j] = E::pack2f(p0, p1);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < DEC_NI / 2; ++j)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        // (v of key 2j, v of key 2j+1) for dims 2w and 2w+1
+        const uint32_t lo = __builtin_amdgcn_perm(R.v[2 * j + 1][w], R.v[2 * j][w], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(R.v[2 * j + 1][w], R.v[2 * j][w], 0x07060302u);
+#pragma unroll
+        for (int h = 0; h < NH; ++h) {
+          acc[h][2 * w] = E::dot2(pp[h][j], lo, acc[h][2 * w]);
+          acc[h][2 * w + 1] = E::dot2(pp[h][j], hi, acc[h][2 * w + 1]);
+        }
+      }
   }
 
   static __device__ void run(const DecodeArgs& a) {
     __shared__ float s_m[DEC_WAVES][NH];
     __shared__ float s_l[DEC_WAVES][NH];
     __shared__ float s_acc[DEC_WAVES][NH][D];
+    __shared__ int32_t s_blk[DEC_CACHE];
+    __shared__ int32_t s_pg[DEC_CACHE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int dc = lane % LPR;  // head-dim chunk
-    const int kg = lane / LPR;  // key row within a load instruction
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     int wid = blockIdx.x;
     const int s = wid % a.num_splits;
@@ -78,24 +197,41 @@ struct Decode {
     const int hs = wid % a.head_splits;
     const int b = wid / a.head_splits;
     const int h0 = r * a.heads_per_row + hs * NH;  // first query head of this workgroup
-    const int kvh = h0 / (a.Hq / a.Hkv);
 
+    Ctx c;
+    c.dc = lane % LPR;  // head-dim chunk
+    c.kg = lane / LPR;  // key row within a load instruction
+    c.b = b;
+    c.kvh = h0 / (a.Hq / a.Hkv);
     const int32_t* offp = a.sel_off + b * a.off_sb + r * a.off_sr;
     const int lo_all = offp[0];
     const int cnt = offp[1] - lo_all;
-    const int lo = lo_all + (int)((int64_t)cnt * s / a.num_splits);
+    c.lo = lo_all + (int)((int64_t)cnt * s / a.num_splits);
     const int hi = lo_all + (int)((int64_t)cnt * (s + 1) / a.num_splits);
-    const int32_t* selp = a.sel + b * a.sel_sb + r * a.sel_sr;
-    const int L = a.kv_lens ? a.kv_lens[b] : a.kv_len;
-    const int rpb = (a.page + CH - 1) / CH;  // rounds per block
+    c.selp = a.sel + b * a.sel_sb + r * a.sel_sr;
+    c.L = a.kv_lens ? a.kv_lens[b] : a.kv_len;
+    c.rpb = (a.page + CH - 1) / CH;  // rounds per block
+    const int nsel = hi - c.lo;
+    c.cached = nsel <= DEC_CACHE;
+    c.s_blk = s_blk;
+    c.s_pg = s_pg;
+    // Stage the list (and its pages) once: the round loop then reads LDS, not dependent HBM loads.
+    if (c.cached)
+      for (int x = tid; x < nsel; x += 64 * DEC_WAVES) {
+        const int lb = c.selp[c.lo + x];
+        int pg = 0;
+        if (a.block_table && lb >= 0 && (int64_t)lb * a.page < c.L) pg = a.block_table[b * a.bt_stride + lb];
+        s_blk[x] = lb;
+        s_pg[x] = pg;
+      }
 
-    float qv[NH][8];
+    uint32_t qp[NH][4];  // this lane's 8 head dims of each query head, packed pairs
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
-      const u32x4 w = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + (h0 + h) * a.q_sh + dc * 8);
-      unpack8(w, qv[h]);
+      const u32x4 w = *reinterpret_cast<const u32x4*>(a.q + b * a.q_sb + (h0 + h) * a.q_sh + c.dc * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) qp[h][e] = w[e];
     }
-
     float m_run[NH], l_run[NH], acc[NH][8];
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
@@ -104,88 +240,23 @@ struct Decode {
 #pragma unroll
       for (int e = 0; e < 8; ++e) acc[h][e] = 0.f;
     }
+    __syncthreads();  // staged list visible
 
-    const int n_items = (hi - lo) * rpb;
-    for (int it = wave; it < n_items; it += DEC_WAVES) {
-      const int lb = selp[lo + it / rpb];
-      const int k0 = (it % rpb) * CH;  // first key of the round in its block
-      // valid keys this round; blocks past kv_len (or negative ids) load nothing
-      const int nkeys = lb < 0 ? 0 : min(min(CH, a.page - k0), L - lb * a.page - k0);
-      if (nkeys <= 0) continue;
-      const elem_t* kb;
-      const elem_t* vb;
-      if (a.block_table) {
-        const int64_t pg = a.block_table[b * a.bt_stride + lb];
-        kb = a.k + pg * a.kv_sb + kvh * a.kv_sh + (int64_t)k0 * a.kv_st;
-        vb = a.v + pg * a.kv_sb + kvh * a.kv_sh + (int64_t)k0 * a.kv_st;
-      } else {
-        const int64_t t0 = (int64_t)lb * a.page + k0;
-        kb = a.k + b * a.kv_sb + kvh * a.kv_sh + t0 * a.kv_st;
-        vb = a.v + b * a.kv_sb + kvh * a.kv_sh + t0 * a.kv_st;
-      }
-      u32x4 kr[DEC_NI], vr[DEC_NI];
-#pragma unroll
-      for (int i = 0; i < DEC_NI; ++i) {
-        const int key = kg + KPI * i;
-        const bool ok = key < nkeys;
-        kr[i] = ok ? *reinterpret_cast<const u32x4*>(kb + key * a.kv_st + dc * 8) : u32x4{0, 0, 0, 0};
-        vr[i] = ok ? *reinterpret_cast<const u32x4*>(vb + key * a.kv_st + dc * 8) : u32x4{0, 0, 0, 0};
-      }
-      // scores: partial dot over this lane's 8 dims, reduced over the LPR lanes of a row
-      float sc[DEC_NI][NH];
-#pragma unroll
-      for (int i = 0; i < DEC_NI; ++i) {
-        float kf[8];
-        unpack8(kr[i], kf);
-#pragma unroll
-        for (int h = 0; h < NH; ++h) {
-          float p = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) p = fmaf(qv[h][e], kf[e], p);
-          sc[i][h] = p;
-        }
-      }
-#pragma unroll
-      for (int msk = 1; msk < LPR; msk <<= 1)
-#pragma unroll
-        for (int i = 0; i < DEC_NI; ++i)
-#pragma unroll
-          for (int h = 0; h < NH; ++h) sc[i][h] += __shfl_xor(sc[i][h], msk, 64);
-
-#pragma unroll
-      for (int h = 0; h < NH; ++h) {
-        float mx = -__builtin_inff();
-#pragma unroll
-        for (int i = 0; i < DEC_NI; ++i) {
-          const float x = (kg + KPI * i < nkeys) ? sc[i][h] * a.scale_log2 : -__builtin_inff();
-          sc[i][h] = x;
-          mx = fmaxf(mx, x);
-        }
-#pragma unroll
-        for (int msk = LPR; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-        const float m_new = fmaxf(m_run[h], mx);
-        const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
-        const float alpha = fast_exp2(m_run[h] - m_use);
-        m_run[h] = m_new;
-        l_run[h] *= alpha;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] *= alpha;
-#pragma unroll
-        for (int i = 0; i < DEC_NI; ++i) {
-          const float p = fast_exp2(sc[i][h] - m_use);
-          l_run[h] += p;
-          sc[i][h] = E::to_f32(E::from_f32(p));  // P rounded to the element type for PV
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < DEC_NI; ++i) {
-        float vf[8];
-        unpack8(vr[i], vf);
-#pragma unroll
-        for (int h = 0; h < NH; ++h)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[h][e] = fmaf(sc[i][h], vf[e], acc[h][e]);
-      }
+    // Rounds it = wave, wave + DEC_WAVES, ...: the next round's loads are issued before the
+    // current round is computed (two register sets, alternating).
+    const int n_items = nsel * c.rpb;
+    Round A, B;
+    int it = wave;
+    if (it < n_items) issue(a, c, it, A);
+    for (;;) {
+      if (it >= n_items) break;
+      if (it + DEC_WAVES < n_items) issue(a, c, it + DEC_WAVES, B);
+      compute(A, qp, a.scale_log2, c.kg, m_run, l_run, acc);
+      it += DEC_WAVES;
+      if (it >= n_items) break;
+      if (it + DEC_WAVES < n_items) issue(a, c, it + DEC_WAVES, A);
+      compute(B, qp, a.scale_log2, c.kg, m_run, l_run, acc);
+      it += DEC_WAVES;
     }
 
     // merge the key rows of the wave (lanes with equal dc), then the waves through LDS
@@ -198,11 +269,11 @@ struct Decode {
         for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], msk, 64);
       }
     // every lane of a row group holds the same sums; lanes 0..LPR-1 publish them
-    if (kg == 0) {
+    if (c.kg == 0) {
 #pragma unroll
       for (int h = 0; h < NH; ++h)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) s_acc[wave][h][dc * 8 + e] = acc[h][e];
+        for (int e = 0; e < 8; ++e) s_acc[wave][h][c.dc * 8 + e] = acc[h][e];
     }
     if (lane == 0) {
 #pragma unroll
@@ -242,8 +313,9 @@ struct Decode {
   }
 };
 
+// At most 256 registers per lane: at least two waves per SIMD.
 template <bool BF16, int D, int NH>
-__global__ __launch_bounds__(64 * DEC_WAVES) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * DEC_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
   Decode<BF16, D, NH>::run(a);
 }
 
