@@ -122,6 +122,25 @@ int64_t sa_prefill_workspace_bytes(void);
  * bit 1 if some query block's ids did not ascend; either makes the schedule
  * unusable.  Nothing is synchronised: read *status after the stream.
  */
+/*
+ * Block mask -> CSR on the GPU: the reference's build_block_pairs_from_mask
+ * (sparse_attentions/patterns/base.py:36-89) applied to a block mask, without
+ * the host round trips of its per-row loop.  mask [rows, nqb, nkb], one byte
+ * per block (nonzero = retained), byte strides mask_row_stride and
+ * mask_qb_stride, key blocks contiguous.  Writes offsets [rows, nqb + 1]
+ * (row stride offsets_stride) and nnz [rows] (retained blocks per row).  With
+ * pairs == NULL this is the count pass; with pairs [rows, width] (row stride
+ * pairs_stride) it also writes the ascending key blocks of every query block
+ * and zero-pads each row to width.  The reference's width is
+ * max(1, max nnz), known after the count pass.  *status (a device int the
+ * caller zeroes) receives 1 if a row holds more than width blocks.
+ */
+int sa_block_mask_to_csr(const uint8_t* mask, int64_t mask_row_stride, int64_t mask_qb_stride,
+                         int rows, int nqb, int nkb,
+                         int32_t* offsets, int64_t offsets_stride, int32_t* nnz,
+                         int32_t* pairs, int64_t pairs_stride, int64_t width,
+                         int* status, void* stream);
+
 int sa_csr_to_tiles(const int32_t* pairs, int64_t pairs_stride,
                     const int32_t* offsets, int64_t offsets_stride,
                     int rows, int nqb, int block_size,

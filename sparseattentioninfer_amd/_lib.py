@@ -40,6 +40,13 @@ SIGNATURES = {
         _vp,
     ]),
     "sa_prefill_workspace_bytes": (_i64, []),
+    "sa_block_mask_to_csr": (_i32, [
+        _vp, _i64, _i64,
+        _i32, _i32, _i32,
+        _vp, _i64, _vp,
+        _vp, _i64, _i64,
+        _vp, _vp,
+    ]),
     "sa_csr_to_tiles": (_i32, [
         _vp, _i64,
         _vp, _i64,

@@ -96,6 +96,33 @@ def csr_to_tiles(block_pairs: torch.Tensor, block_pair_offsets: torch.Tensor, bl
     return TileSchedule(tp, tm, to, status, block_size)
 
 
+def block_mask_to_csr_gpu(block_active: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """``[R, NQB, NKB]`` bool block mask on the GPU -> the reference's ``(pairs, offsets)``.
+
+    Count pass, one read of the widest row (the reference pads every row to
+    ``max(1, max nnz)``), write pass; bit-identical to the torch packing.
+    """
+    name = "block_mask_to_csr"
+    _require(block_active.is_cuda and block_active.dim() == 3, f"{name}: needs a [R, NQB, NKB] GPU tensor")
+    m = block_active.to(torch.uint8) if block_active.dtype != torch.uint8 else block_active
+    if m.stride(2) != 1:
+        m = m.contiguous()
+    R, nqb, nkb = m.shape
+    dev = m.device
+    offsets = torch.empty(R, nqb + 1, dtype=torch.int32, device=dev)
+    nnz = torch.empty(R, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    args = (m.data_ptr(), m.stride(0), m.stride(1), R, nqb, nkb, offsets.data_ptr(), offsets.stride(0),
+            nnz.data_ptr())
+    _lib.check(name, lib.sa_block_mask_to_csr(*args, None, 0, 0, None, _stream(m)))
+    width = max(1, int(nnz.max().item())) if R else 1
+    pairs = torch.empty(R, width, dtype=torch.int32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    _lib.check(name, lib.sa_block_mask_to_csr(*args, pairs.data_ptr(), pairs.stride(0), width,
+                                              status.data_ptr(), _stream(m)))
+    return pairs, offsets
+
+
 def _schedule_args(pairs, offsets, block_size, tiles: TileSchedule | None):
     """Schedule arguments of sa_prefill: (pairs, offsets, masks) tensors to keep alive, the six
     pointer/stride arguments, and the number of schedule query blocks."""

@@ -73,7 +73,14 @@ def _pack_flat(rows: torch.Tensor, vals: torch.Tensor, counts: torch.Tensor, nqb
 
 
 def block_mask_to_csr(block_active: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """``[R, NQB, NKB]`` bool -> ``(pairs, offsets)`` in the reference's CSR format."""
+    """``[R, NQB, NKB]`` bool -> ``(pairs, offsets)`` in the reference's CSR format.
+
+    GPU masks go through the HIP builder (``ops.block_mask_to_csr_gpu``); CPU
+    masks are packed with torch.  Both give the same bits.
+    """
+    if block_active.is_cuda:
+        from ..ops import block_mask_to_csr_gpu
+        return block_mask_to_csr_gpu(block_active)
     R, nqb, nkb = block_active.shape
     per_row = block_active.sum(dim=2)                       # [R, NQB]
     counts = per_row.sum(dim=1)                             # [R]

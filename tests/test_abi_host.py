@@ -28,7 +28,7 @@ def lib():
 
 def test_header_declares_entry_points():
     assert {"sa_abi_version", "sa_last_error", "sa_prefill", "sa_prefill_workspace_bytes", "sa_decode",
-            "sa_decode_workspace_bytes", "sa_csr_to_tiles"} <= _declared()
+            "sa_decode_workspace_bytes", "sa_csr_to_tiles", "sa_block_mask_to_csr"} <= _declared()
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -58,6 +58,11 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     st = lib.sa_csr_to_tiles(None, 0, None, 0, 2, 4, 64, None, None, 0, 4, None, 0, None, None)
     assert st == -4 and b"not 16 or 32" in lib.sa_last_error()
     st = lib.sa_csr_to_tiles(None, 0, None, 0, 2, 4, 16, None, None, 0, 4, None, 0, None, None)
+    assert st == -6
+    # GPU CSR builder: the write pass needs a width and a status word; NULL mask refused
+    st = lib.sa_block_mask_to_csr(None, 0, 0, 2, 4, 4, None, 0, None, 8, 4, 0, None, None)
+    assert st == -2 and b"width >= 1" in lib.sa_last_error()
+    st = lib.sa_block_mask_to_csr(None, 0, 0, 2, 4, 4, None, 0, None, None, 0, 0, None, None)
     assert st == -6
     st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, None, 0, None, 0, 0, None, 0, 0,
                        3, None, 0, 0, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
