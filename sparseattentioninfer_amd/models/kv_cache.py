@@ -96,6 +96,11 @@ class KVCache:
         """Forgets the cached tokens; the buffers are kept for reuse."""
         self._len = [0] * self.num_layers
 
+    def truncate(self, length: int) -> None:
+        """Drops every layer's tokens past ``length`` (no copy): a benchmark's decode step can
+        restart from the same prefix."""
+        self._len = [min(n, length) for n in self._len]
+
     def get(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
         """The cached ``[B, H, T, D]`` views of one layer."""
         if self._kbuf[layer_idx] is None:
