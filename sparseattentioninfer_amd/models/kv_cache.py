@@ -131,25 +131,37 @@ class PagedKVStore:
         self.kv_lens = torch.zeros(batch, dtype=torch.int32, device=device)
         self.lens = [0] * batch
         self._table_host = [[] for _ in range(batch)]
+        self._page_cols: dict = {}
         order = torch.arange(self.num_pages)
         if shuffle_seed is not None:
             order = order[torch.randperm(self.num_pages, generator=torch.Generator().manual_seed(shuffle_seed))]
         self._free = order.tolist()[::-1]   # pop() hands out order[0] first
 
-    def _grow(self, b: int, new_len: int) -> None:
+    def _grow_all(self, new_len: int) -> None:
+        """Gives every sequence the pages that ``new_len`` tokens need (one table update)."""
         need = -(-new_len // self.page)
         if need > self.max_blocks:
-            raise ValueError(f"sequence {b} needs {need} blocks > max_blocks {self.max_blocks}")
-        row = self._table_host[b]
+            raise ValueError(f"sequences need {need} blocks > max_blocks {self.max_blocks}")
+        have = len(self._table_host[0])
+        if need <= have:
+            return
+        if len(self._free) < self.batch * (need - have):
+            raise RuntimeError("paged KV cache: out of pages")
         added = []
-        while len(row) < need:
-            if not self._free:
-                raise RuntimeError("paged KV cache: out of pages")
-            row.append(self._free.pop())
-            added.append(row[-1])
-        if added:
-            start = len(row) - len(added)
-            self.block_table[b, start:len(row)] = torch.tensor(added, dtype=torch.int32)
+        for row in self._table_host:
+            for _ in range(need - have):
+                row.append(self._free.pop())
+            added.append(row[have:need])
+        self.block_table[:, have:need] = torch.tensor(added, dtype=torch.int32).to(self.block_table.device)
+        self._page_cols.clear()
+
+    def _page_col(self, lb: int) -> torch.Tensor:
+        """Pages of logical block ``lb`` for every sequence, as a device index tensor (cached)."""
+        col = self._page_cols.get(lb)
+        if col is None:
+            col = self.block_table[:, lb].long()
+            self._page_cols[lb] = col
+        return col
 
     def write(self, k_new: torch.Tensor, v_new: torch.Tensor) -> None:
         """Appends ``[B, H, t, D]`` K/V at every sequence's end (all sequences advance by t)."""
@@ -158,16 +170,19 @@ class PagedKVStore:
             raise ValueError(f"write of {tuple(k_new.shape)} into a [{self.batch}, {self.heads}, *, "
                              f"{self.head_dim}] store")
         start = self.lens[0]
-        if any(n != start for n in self.lens):
-            raise ValueError("write() advances all sequences together; their lengths differ")
-        for b in range(B):
-            self._grow(b, start + t)
-        pos = torch.arange(start, start + t, device=k_new.device)
-        pages = self.block_table[:, pos // self.page].long()          # [B, t]
-        slots = (pos % self.page).expand(B, t)                         # [B, t]
-        # advanced indices on dims 0 and 2 put [B, t] first: [B, t, H, D]
-        self.k_pages[pages, :, slots] = k_new.transpose(1, 2).to(self.k_pages.dtype)
-        self.v_pages[pages, :, slots] = v_new.transpose(1, 2).to(self.v_pages.dtype)
+        self._grow_all(start + t)
+        if t == 1:   # decode: one slot of one page per sequence
+            idx = self._page_col(start // self.page)
+            slot = start % self.page
+            self.k_pages[idx, :, slot] = k_new[:, :, 0].to(self.k_pages.dtype)
+            self.v_pages[idx, :, slot] = v_new[:, :, 0].to(self.v_pages.dtype)
+        else:
+            pos = torch.arange(start, start + t, device=k_new.device)
+            pages = self.block_table[:, pos // self.page].long()          # [B, t]
+            slots = (pos % self.page).expand(B, t)                         # [B, t]
+            # advanced indices on dims 0 and 2 put [B, t] first: [B, t, H, D]
+            self.k_pages[pages, :, slots] = k_new.transpose(1, 2).to(self.k_pages.dtype)
+            self.v_pages[pages, :, slots] = v_new.transpose(1, 2).to(self.v_pages.dtype)
         self.lens = [start + t] * B
         self.kv_lens.fill_(start + t)
 
@@ -188,5 +203,6 @@ class PagedKVStore:
         for row in self._table_host:
             self._free.extend(reversed(row))
             row.clear()
+        self._page_cols.clear()
         self.lens = [0] * self.batch
         self.kv_lens.zero_()
