@@ -120,6 +120,22 @@ __device__ __forceinline__ void load_lds16(const void* vaddr, uint32_t lds) {
 // Waits for the calling wave's direct loads (and any other vector memory access).
 __device__ __forceinline__ void wait_dma() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 
+// Wave-uniform 32-bit global read that has completed when it returns (it waits for every
+// vector memory access of the wave).  For the rare reads of a CSR row past its LDS cache:
+// written as one opaque block, it leaves the compiler no pending load into a register that
+// the LDS path reuses, which would otherwise make every LDS read of the row wait for the
+// direct loads.
+__device__ __forceinline__ int32_t load_uniform_now(const int32_t* p) {
+  int32_t x;
+  asm volatile(
+      "global_load_dword %0, %1, off\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=v"(x)
+      : "v"(p)
+      : "memory");
+  return __builtin_amdgcn_readfirstlane(x);
+}
+
 // SUB: tile schedules with sub-block masks (block sizes 16 and 32); without it the mask
 // bookkeeping compiles away.
 template <bool BF16, int D, int HW, bool SUB>
@@ -132,12 +148,12 @@ struct Prefill {
   static constexpr int NI = TILE_BYTES / 1024;   // 1 KiB wave-wide direct loads per tile
   static constexpr int NIW = NI / NW;            // ... issued by each wave
   static constexpr int WAVE_BYTES = QT * D * 2;  // 32 rows of Q or O (one wave's share)
-  // Four-head workgroups run the software-pipelined loop with K triple- and V double-
+  // Four-head workgroups run the software-pipelined loop with K double- and V triple-
   // buffered and Q staged in LDS.  Other shapes run one tile at a time over double-buffered
   // K/V (single-buffered for one-head workgroups, so that more of them share a CU).
   static constexpr bool PIPE = HW == 4;
-  static constexpr int NBK = PIPE ? 3 : (HW == 1 ? 1 : 2);
-  static constexpr int NBV = PIPE ? 2 : NBK;
+  static constexpr int NBK = PIPE ? 2 : (HW == 1 ? 1 : 2);
+  static constexpr int NBV = PIPE ? 3 : NBK;
   static constexpr int LDS_KV = (NBK + NBV) * TILE_BYTES;
   static constexpr int LDS_Q = PIPE ? NW * WAVE_BYTES : 16;
   static constexpr float RESCALE_LOG2 = 8.f;
@@ -266,12 +282,15 @@ struct Prefill {
     int q_row0, q_abs_tile_max, q_abs_min;
   };
 
-  // Sets up work item (qt, r, hs, b): query tile qt (64 rows) of CSR row r, batch b, head
-  // split hs.  Each wave owns 32 rows (half hf) of one query head; every K/V tile staged in
-  // LDS feeds all NW waves.  Caches the CSR row of the query tile in s_row (callers barrier
-  // before, so no wave still reads it).
-  static __device__ __forceinline__ Item setup(const PrefillArgs& a, int qt, int r, int hs, int b, int32_t* s_row,
-                                               int32_t* s_mask) {
+  // CSR entries of one row cached in LDS.  The persistent four-head loop keeps two rows
+  // (this item's and the next one's), so tile schedules, which also cache their masks, hold
+  // fewer entries per row there.
+  static constexpr int RC = (PIPE && SUB) ? ROW_CACHE / 2 : ROW_CACHE;
+
+  // Work item (qt, r, hs, b) whose CSR row holds entries [e0, e0 + n_ent): pointers and
+  // positions only, no memory reads.
+  static __device__ __forceinline__ Item setup_base(const PrefillArgs& a, int qt, int r, int hs, int b, int e0,
+                                                    int n_ent) {
     Item it;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -285,26 +304,35 @@ struct Prefill {
     it.qb = a.q + b * a.q_sb + it.hq * a.q_sh;
     it.kb = a.k + b * a.k_sb + kvh * a.k_sh;
     it.vb = a.v + b * a.v_sb + kvh * a.v_sh;
-
-    // CSR row of this query tile; each block holds 2^tpb_log2 key tiles.
-    const int qblk = qt >> a.qpb_log2;
-    const int32_t* offs = a.offsets + r * a.offsets_stride;
     it.prow = a.pairs + r * a.pairs_stride;
     it.mrow = SUB ? a.tile_masks + r * a.masks_stride : nullptr;
-    it.e0 = offs[qblk];
-    const int n_ent = offs[qblk + 1] - it.e0;
-    it.cached = n_ent <= ROW_CACHE;
-    if (it.cached) {
-      for (int x = tid; x < n_ent; x += NT) s_row[x] = it.prow[it.e0 + x];
-      if (SUB)
-        for (int x = tid; x < n_ent; x += NT) s_mask[x] = it.mrow[it.e0 + x];
-    }
+    it.e0 = e0;
+    it.cached = n_ent <= RC;
     it.n_tiles = n_ent << a.tpb_log2;
     it.tpb_mask = (1 << a.tpb_log2) - 1;
     const int q_tile0 = qt * QTILE;
     it.q_row0 = q_tile0 + QT * it.hf;  // this wave's first row
     it.q_abs_tile_max = a.q_offset + min(a.Tq, q_tile0 + QTILE) - 1;
     it.q_abs_min = a.q_offset + it.q_row0;  // this wave's first absolute position
+    return it;
+  }
+
+  // Sets up work item (qt, r, hs, b): query tile qt (64 rows) of CSR row r, batch b, head
+  // split hs.  Each wave owns 32 rows (half hf) of one query head; every K/V tile staged in
+  // LDS feeds all NW waves.  Caches the CSR row of the query tile in s_row (callers barrier
+  // before, so no wave still reads it).
+  static __device__ __forceinline__ Item setup(const PrefillArgs& a, int qt, int r, int hs, int b, int32_t* s_row,
+                                               int32_t* s_mask) {
+    // CSR row of this query tile; each block holds 2^tpb_log2 key tiles.
+    const int32_t* offs = a.offsets + r * a.offsets_stride + (qt >> a.qpb_log2);
+    const int e0 = offs[0];
+    const Item it = setup_base(a, qt, r, hs, b, e0, offs[1] - e0);
+    if (it.cached) {
+      const int n_ent = it.n_tiles >> a.tpb_log2;
+      for (int x = threadIdx.x; x < n_ent; x += NT) s_row[x] = it.prow[e0 + x];
+      if (SUB)
+        for (int x = threadIdx.x; x < n_ent; x += NT) s_mask[x] = it.mrow[e0 + x];
+    }
     return it;
   }
 
@@ -316,11 +344,9 @@ struct Prefill {
 
   static __device__ __forceinline__ int tile_of(const PrefillArgs& a, const Item& it, const int32_t* s_row, int t) {
     const int e = t >> a.tpb_log2;
-    // Two distinct loads (LDS cache, or a global read past ROW_CACHE entries); the global
-    // one is a relaxed atomic so the two are not merged into one flat load of a selected
-    // pointer (a flat load would also wait for the in-flight direct loads).
-    const int blk = it.cached ? s_row[e]
-                              : __hip_atomic_load(it.prow + it.e0 + e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Two distinct loads (LDS cache, or a global read past the cached entries), so the two are
+    // not merged into one flat load of a selected pointer.
+    const int blk = it.cached ? s_row[e] : load_uniform_now(it.prow + it.e0 + e);
     return (blk << a.tpb_log2) + (t & it.tpb_mask);
   }
 
@@ -328,8 +354,7 @@ struct Prefill {
 
   // Sub-block mask of schedule position t (tile schedules only; t indexes entries there).
   static __device__ __forceinline__ uint32_t mask_of(const Item& it, const int32_t* s_mask, int t) {
-    return (uint32_t)(it.cached ? s_mask[t]
-                                : __hip_atomic_load(it.mrow + it.e0 + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return (uint32_t)(it.cached ? s_mask[t] : load_uniform_now(it.mrow + it.e0 + t));
   }
 
   // Whether a sub-block mask drops any sub-block of its tile.
@@ -592,19 +617,99 @@ struct Prefill {
     return m == -__builtin_inff() ? 0.f : -m;
   }
 
+  // ---- lookahead metadata (persistent four-head loop) -----------------------------------
+  // While an item's first tiles load, the persistent loop fetches the CSR row of the next
+  // item, the CSR offsets of the item after it and a new claim from the counter.  All of it
+  // lands in LDS before the barrier that publishes the item's first tiles, so the next item
+  // starts without a dependent global read and no register stays live across the tile loop.
+  struct Look {
+    int e0, n_ent;        // this item's CSR entries
+    int v1, e0_1, n_1;    // next item (>= n_items: none) and its CSR entries
+    int v2;               // the item after it
+    int n_items;
+    int32_t* row_dst;     // row cache of the next item (and its sub-block masks)
+    int32_t* mask_dst;
+    int* off_dst;         // CSR offsets (first, end) of item v2
+    int* vid_dst;         // slot of the newly claimed item
+  };
+  static constexpr int RPT = (RC + NT - 1) / NT;  // cached row entries per thread
+  struct LookLoads {
+    int32_t rv[RPT];
+    int32_t mv[SUB ? RPT : 1];
+    int o0, o1;
+    unsigned nv;
+  };
+
+  // Offsets entry of item v's query block in its CSR row.
+  static __device__ __forceinline__ const int32_t* offsets_ptr(const PrefillArgs& a, int v) {
+    int qt, r, hs, b;
+    decode_item(a, v, qt, r, hs, b);
+    return a.offsets + r * a.offsets_stride + (qt >> a.qpb_log2);
+  }
+
+  static __device__ __forceinline__ void look_issue(const PrefillArgs& a, const Look& lk, LookLoads& ld) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < RPT; ++u) ld.rv[u] = ld.mv[SUB ? u : 0] = 0;
+    ld.o0 = ld.o1 = 0;
+    ld.nv = 0;
+    if (lk.v1 < lk.n_items && lk.n_1 <= RC) {
+      int qt, r, hs, b;
+      decode_item(a, lk.v1, qt, r, hs, b);
+      const int32_t* src = a.pairs + r * a.pairs_stride + lk.e0_1;
+#pragma unroll
+      for (int u = 0; u < RPT; ++u)
+        if (tid + u * NT < lk.n_1) ld.rv[u] = src[tid + u * NT];
+      if (SUB) {
+        const int32_t* msrc = a.tile_masks + r * a.masks_stride + lk.e0_1;
+#pragma unroll
+        for (int u = 0; u < RPT; ++u)
+          if (tid + u * NT < lk.n_1) ld.mv[u] = msrc[tid + u * NT];
+      }
+    }
+    if (tid == 0) {
+      if (lk.v2 < lk.n_items) {
+        const int32_t* o = offsets_ptr(a, lk.v2);
+        ld.o0 = o[0];
+        ld.o1 = o[1];
+      }
+      ld.nv = atomicAdd(a.counter, 1u);
+    }
+  }
+
+  static __device__ __forceinline__ void look_commit(const Look& lk, const LookLoads& ld) {
+    const int tid = threadIdx.x;
+    if (lk.v1 < lk.n_items && lk.n_1 <= RC) {
+#pragma unroll
+      for (int u = 0; u < RPT; ++u)
+        if (tid + u * NT < lk.n_1) {
+          lk.row_dst[tid + u * NT] = ld.rv[u];
+          if (SUB) lk.mask_dst[tid + u * NT] = ld.mv[u];
+        }
+    }
+    if (tid == 0) {
+      lk.off_dst[0] = ld.o0;
+      lk.off_dst[1] = ld.o1;
+      lk.vid_dst[0] = (int)ld.nv;
+    }
+  }
+
   // Same work item as item(), with the tile loop software-pipelined: each step computes the
   // probabilities of tile i while the matrix cores already run S^T = K Q^T of tile i+1,
   // then O^T += V^T P^T of tile i while the VALU reduces the row max of tile i+1.
   // Meanwhile the direct loads fetch K of tile i+2 (three K buffers) and V of tile i+1 (two
   // V buffers).  Tiles that lie wholly after this wave's rows cost matrix work but add
-  // p == 0.
+  // p == 0.  LOOK: the item's CSR row is already in s_row (lk->e0, lk->n_ent) and the
+  // lookahead reads of *lk run under the first tiles' loads.
+  template <bool LOOK>
   static __device__ __forceinline__ void item_pipelined(const PrefillArgs& a, int qt, int r, int hs, int b,
-                                                        char* sKV, char* sQ, int32_t* s_row, int32_t* s_mask) {
+                                                        char* sKV, char* sQ, int32_t* s_row, int32_t* s_mask,
+                                                        const Look* lk) {
     char* sK = sKV;
     char* sV = sKV + NBK * TILE_BYTES;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const Item it = setup(a, qt, r, hs, b, s_row, s_mask);
+    const Item it = LOOK ? setup_base(a, qt, r, hs, b, lk->e0, lk->n_ent) : setup(a, qt, r, hs, b, s_row, s_mask);
     const char* sQw = sQ + wave * WAVE_BYTES;
     {  // Q^T operand of this wave into LDS, in fragment order
       const elem_t* qs = q_src(a, it);
@@ -615,7 +720,7 @@ struct Prefill {
     const DmaLane dl(a, lane);
     // lim of tile kt: min(q_abs, T_k - 1) - kt*KT - 8g (past the tile when no key is masked)
     const int lim0 = min(it.q_abs_min + it.l32, a.Tk - 1) - 8 * it.g;
-    __syncthreads();  // s_row visible
+    if (!LOOK) __syncthreads();  // s_row visible (LOOK: it was before the item began)
 
     f32x16 O[D / 32];
 #pragma unroll
@@ -638,7 +743,10 @@ struct Prefill {
       dma<false>(it.vb, a.v_st, dl.v, sV, kt_cur, a.Tk, wave, lane);
     }
     if (t_nxt < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+    LookLoads ld;
+    if constexpr (LOOK) look_issue(a, *lk, ld);
     wait_dma();
+    if constexpr (LOOK) look_commit(*lk, ld);
     __syncthreads();
     f32x16 S[2] = {f32x16{}, f32x16{}};  // scores of the current tile
     float mt_cur = -__builtin_inff();
@@ -651,21 +759,65 @@ struct Prefill {
       }
       mt_cur = mask_rowmax(a, S, row_bits(a, m_cur, it.hf, it.l32), lim0 - kt_cur * KT, c);
     }
+    // The first step loads K of tile t2 into the buffer of t0, which the prime just read.
+    __syncthreads();
 
-    int kb_cur = 0;  // K buffer of the current tile (tile t_nxt's is kb_cur + 1 mod 3)
-    int vb_cur = 0;  // V buffer of the current tile
-    // One pipeline step on the tile in S (this tile) while filling Sn (next tile).
+    // Each step holds two half-steps per wave: A = S^T of the next tile on the matrix cores
+    // under the exponentials of this tile, B = O^T += V^T P^T of a tile under the row max of
+    // the following one.  The lower 32-row half runs A(i), B(i) in step i; the upper half
+    // runs B(i-1), A(i), so the two waves on each SIMD (one of each half) run the VALU-heavy
+    // A and the matrix-only B at the same time.  K is double-buffered (K of tile i+1 is read
+    // in step i by both halves, K of tile i+2 loads); V is triple-buffered (V of tiles i-1
+    // and i are read, V of tile i+1 loads), so one barrier per step still suffices.
+    const bool lag = it.hf == 1;  // upper half: one half-step behind
+    int kb_cur = 0;  // K buffer of the current tile (the next tile's is kb_cur ^ 1)
+    int vb_cur = 0;  // V buffer of the current tile (tile i in buffer i mod 3)
+    bool pending = false;  // upper half: B of the previous tile still to run
+    u32x4 P[2][2];         // probabilities of the tile whose B is next
+    constexpr int NQ = D / 8;    // QK MFMAs per tile: i -> (key half j = i % 2, cc = i / 2)
+    constexpr int PE = 32 / NQ;  // probabilities per QK MFMA
+    constexpr int NP = D / 8;    // PV MFMAs: i -> (dt = i % (D/32), h, j)
+    constexpr int ND = D / 32;
+    constexpr int ME = 32 / NP;  // scores reduced per PV MFMA
+
+    // Block B: PV of the tile in V buffer cV with probabilities P (D/8 MFMAs; V fragments
+    // read two MFMAs ahead), with the scaled row max of R (masked scores) spread over it.
+    auto block_b = [&](const char* cV, const f32x16 (&R)[2]) -> float {
+      auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
+      u32x4 vf[2] = {vfr(0), vfr(1)};
+      float mx = -__builtin_inff();
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        O[i % ND] = E::mfma32(vf[i & 1], P[i / (2 * ND)][(i / ND) & 1], O[i % ND]);
+        if (i + 2 < NP) vf[i & 1] = vfr(i + 2);
+#pragma unroll
+        for (int u = 0; u < ME; ++u) {
+          const int x = ME * i + u;
+          mx = fmaxf(mx, R[x >> 4][x & 15]);
+        }
+        asm volatile("" : "+v"(mx));  // keeps the reduction spread over the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      mx = fmaxf(mx, swap_halves(mx));
+      return mx * c;
+    };
+
     while (t_cur < n_tiles) {
-      const int kb_nxt = kb_cur == 2 ? 0 : kb_cur + 1;
-      const int kb_nn = kb_nxt == 2 ? 0 : kb_nxt + 1;
+      const int kb_nxt = kb_cur ^ 1;
+      const int vb_prev = vb_cur == 0 ? 2 : vb_cur - 1;
+      const int vb_nxt = vb_cur == 2 ? 0 : vb_cur + 1;
       const int t_nn = t_nxt < n_tiles ? next_usable(a, it, s_row, t_nxt + 1) : n_tiles;
       const int kt_nn = t_nn < n_tiles ? tile_of(a, it, s_row, t_nn) : 0;
       const uint32_t m_nn = sub_log2(a) && t_nn < n_tiles ? mask_of(it, s_mask, t_nn) : 0u;
-      if (t_nn < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + kb_nn * TILE_BYTES, kt_nn, a.Tk, wave, lane);
-      if (t_nxt < n_tiles) dma<false>(it.vb, a.v_st, dl.v, sV + (vb_cur ^ 1) * TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+      if (t_nn < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + kb_cur * TILE_BYTES, kt_nn, a.Tk, wave, lane);
+      if (t_nxt < n_tiles) dma<false>(it.vb, a.v_st, dl.v, sV + vb_nxt * TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+
+      // Upper half: B of the previous tile; the row max it reduces is this tile's.
+      if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, S);
+
       const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
-      u32x4 P[2][2];
-      const char* cV = sV + vb_cur * TILE_BYTES;
       const char* cK = sK + kb_nxt * TILE_BYTES;
       // Branch-free on purpose: after the last tile the QK half runs on a stale K buffer
       // (no direct load is in flight then) and its result is dropped.  A separate last-tile
@@ -676,17 +828,14 @@ struct Prefill {
       // fragments two chunk pairs ahead) with this tile's probabilities spread over it.
       // The sched_barrier fences keep the order as written: one MFMA, its LDS reads, its
       // share of the VALU work.
-      constexpr int NQ = D / 8;    // QK MFMAs per tile: i -> (key half j = i % 2, cc = i / 2)
-      constexpr int PE = 32 / NQ;  // probabilities per QK MFMA
       auto kfr = [&](int i) { return kfrag(cK, f, i & 1, i >> 1); };
       u32x4 kf[3] = {kfr(0), kfr(1), kfr(2)};
       u32x4 qv[2] = {qfrag(sQw, lane, 0), qfrag(sQw, lane, 1)};
       f32x16 Sn[2] = {f32x16{}, f32x16{}};
       float ls = 0.f;
       uint32_t pw[2][2][4];
-      // The two waves of a SIMD run the same step; raising the priority of the one in the
-      // VALU-heavy block A lets its exponentials go first while the other wave's matrix
-      // instructions fill the MFMA pipe (about 5% faster than equal priorities).
+      // Raising the priority of the wave in the VALU-heavy block A lets its exponentials go
+      // first while the other wave's matrix instructions fill the MFMA pipe.
       __builtin_amdgcn_s_setprio(1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -722,30 +871,9 @@ struct Prefill {
         mask_tile(a, Sn, row_bits(a, m_nxt, it.hf, it.l32), lim0 - kbase_n);
       }
 
-      // Block B: PV of this tile (D/8 MFMAs; V fragments read two MFMAs ahead) with the
-      // next tile's row max spread over it.
-      constexpr int NP = D / 8;  // PV MFMAs: i -> (dt = i % (D/32), h, j)
-      constexpr int ND = D / 32;
-      constexpr int ME = 32 / NP;  // scores reduced per PV MFMA
-      auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
-      u32x4 vf[2] = {vfr(0), vfr(1)};
-      float mx = -__builtin_inff();
-      __builtin_amdgcn_s_setprio(0);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        O[i % ND] = E::mfma32(vf[i & 1], P[i / (2 * ND)][(i / ND) & 1], O[i % ND]);
-        if (i + 2 < NP) vf[i & 1] = vfr(i + 2);
-#pragma unroll
-        for (int u = 0; u < ME; ++u) {
-          const int x = ME * i + u;
-          mx = fmaxf(mx, Sn[x >> 4][x & 15]);
-        }
-        asm volatile("" : "+v"(mx));  // keeps the reduction spread over the MFMAs
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      mx = fmaxf(mx, swap_halves(mx));
-      mt_cur = mx * c;
+      // Lower half: B of this tile; the row max it reduces is the next tile's.
+      if (!lag) mt_cur = block_b(sV + vb_cur * TILE_BYTES, Sn);
+      pending = true;
 
       S[0] = Sn[0];
       S[1] = Sn[1];
@@ -757,9 +885,12 @@ struct Prefill {
       kt_nxt = kt_nn;
       m_nxt = m_nn;
       kb_cur = kb_nxt;
-      vb_cur ^= 1;
+      vb_cur = vb_nxt;
     }
-    // Every wave has passed the last barrier: the K/V buffers are free for the staging.
+    // Upper half: B of the last tile (its V buffer is not reloaded after the last step).
+    if (lag && pending) block_b(sV + (vb_cur == 0 ? 2 : vb_cur - 1) * TILE_BYTES, S);
+    // Every wave is past its last read of the K/V buffers: they are free for the staging.
+    __syncthreads();
     epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
   }
 
@@ -779,16 +910,84 @@ struct Prefill {
     int qt, r, hs, b;
     decode_item(a, v, qt, r, hs, b);
     if constexpr (PIPE)
-      item_pipelined(a, qt, r, hs, b, sKV, sQ, s_row, s_mask);
+      item_pipelined<false>(a, qt, r, hs, b, sKV, sQ, s_row, s_mask, nullptr);
     else
       item(a, qt, r, hs, b, sKV, s_row, s_mask);
+  }
+
+  // Persistent four-head loop with lookahead.  Item i of this workgroup finds in LDS its id
+  // (s_vid[i % 4]), its CSR offsets (s_off[i % 4]) and row (row cache i % 2), and the id and
+  // offsets of item i + 1 and the id of item i + 2; its prologue fetches the row of item
+  // i + 1, the offsets of item i + 2 and claims item i + 3 (Look).  Claims only grow, so the
+  // first id past the end ends the loop in every wave at once.
+  static __device__ __forceinline__ void run_lookahead(const PrefillArgs& a, int n_items, char* sKV, char* sQ,
+                                                       int32_t* s_row, int32_t* s_mask) {
+    __shared__ int s_vid[4];
+    __shared__ int s_off[8];
+    const int tid = threadIdx.x;
+    if (tid == 0) {
+      const unsigned v0 = atomicAdd(&a.counter[0], 1u);
+      const unsigned v1 = atomicAdd(&a.counter[0], 1u);
+      const unsigned v2 = atomicAdd(&a.counter[0], 1u);
+      s_vid[0] = (int)v0;
+      s_vid[1] = (int)v1;
+      s_vid[2] = (int)v2;
+    }
+    __syncthreads();
+    if (tid < 2) {
+      const int v = s_vid[tid];
+      if (v < n_items) {
+        const int32_t* o = offsets_ptr(a, v);
+        s_off[2 * tid] = o[0];
+        s_off[2 * tid + 1] = o[1];
+      }
+    }
+    __syncthreads();
+    {
+      const int v = s_vid[0];
+      const int e0 = s_off[0], n = s_off[1] - e0;
+      if (v < n_items && n <= RC) {
+        int qt, r, hs, b;
+        decode_item(a, v, qt, r, hs, b);
+        for (int x = tid; x < n; x += NT) {
+          s_row[x] = a.pairs[r * a.pairs_stride + e0 + x];
+          if (SUB) s_mask[x] = a.tile_masks[r * a.masks_stride + e0 + x];
+        }
+      }
+    }
+    for (int i = 0;; ++i) {
+      // Publishes the metadata of item i and frees the K/V buffers (O staging of item i - 1).
+      __syncthreads();
+      // Values read from LDS are the same in every lane; readfirstlane lets the compiler keep
+      // them (and the addresses derived from them) in scalar registers.
+      const int v = __builtin_amdgcn_readfirstlane(s_vid[i & 3]);
+      if (v >= n_items) break;
+      Look lk;
+      lk.e0 = __builtin_amdgcn_readfirstlane(s_off[2 * (i & 3)]);
+      lk.n_ent = __builtin_amdgcn_readfirstlane(s_off[2 * (i & 3) + 1]) - lk.e0;
+      lk.v1 = __builtin_amdgcn_readfirstlane(s_vid[(i + 1) & 3]);
+      lk.e0_1 = __builtin_amdgcn_readfirstlane(s_off[2 * ((i + 1) & 3)]);
+      lk.n_1 = __builtin_amdgcn_readfirstlane(s_off[2 * ((i + 1) & 3) + 1]) - lk.e0_1;
+      lk.v2 = __builtin_amdgcn_readfirstlane(s_vid[(i + 2) & 3]);
+      lk.n_items = n_items;
+      lk.row_dst = s_row + ((i + 1) & 1) * RC;
+      lk.mask_dst = SUB ? s_mask + ((i + 1) & 1) * RC : s_mask;
+      lk.off_dst = s_off + 2 * ((i + 2) & 3);
+      lk.vid_dst = s_vid + ((i + 3) & 3);
+      int qt, r, hs, b;
+      decode_item(a, v, qt, r, hs, b);
+      item_pipelined<true>(a, qt, r, hs, b, sKV, sQ, s_row + (i & 1) * RC, SUB ? s_mask + (i & 1) * RC : s_mask,
+                           &lk);
+    }
   }
 
   static __device__ void run(const PrefillArgs& a) {
     __shared__ __attribute__((aligned(16))) char sKV[LDS_KV];
     __shared__ __attribute__((aligned(16))) char sQ[LDS_Q];
-    __shared__ int32_t s_row[ROW_CACHE];
-    __shared__ int32_t s_mask[SUB ? ROW_CACHE : 1];  // sub-block masks of the cached row
+    // Row caches: two for the persistent four-head loop (this item and the next one).
+    constexpr int NROW = PIPE ? 2 : 1;
+    __shared__ int32_t s_row[NROW * RC];
+    __shared__ int32_t s_mask[SUB ? NROW * RC : 1];  // sub-block masks of the cached rows
     __shared__ int s_item;
     const int n_items = a.ntq * a.R * a.B * a.head_splits;
 
@@ -809,13 +1008,17 @@ struct Prefill {
     // Persistent: claim items from a counter until none is left.  The last workgroup to
     // finish resets the counter pair to zero for the next launch on the stream.  The
     // barriers also separate one item's epilogue (LDS staging) from the next item's loads.
-    for (;;) {
-      if (threadIdx.x == 0) s_item = (int)atomicAdd(&a.counter[0], 1u);
-      __syncthreads();
-      const int v = s_item;
-      __syncthreads();
-      if (v >= n_items) break;
-      process(a, v, sKV, sQ, s_row, s_mask);
+    if constexpr (PIPE) {
+      run_lookahead(a, n_items, sKV, sQ, s_row, s_mask);
+    } else {
+      for (;;) {
+        if (threadIdx.x == 0) s_item = (int)atomicAdd(&a.counter[0], 1u);
+        __syncthreads();
+        const int v = s_item;
+        __syncthreads();
+        if (v >= n_items) break;
+        process(a, v, sKV, sQ, s_row, s_mask);
+      }
     }
     if (threadIdx.x == 0 && atomicAdd(&a.counter[1], 1u) == gridDim.x - 1) {
       atomicExch(&a.counter[0], 0u);
