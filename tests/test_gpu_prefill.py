@@ -163,7 +163,8 @@ def test_persistent_and_grid_launches_agree_and_reset_workspace():
     pairs, offsets = (x.to(DEV) for x in block_mask_to_csr(bm))
     q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=12))
     lib = _lib.load()
-    ws = torch.zeros(2, dtype=torch.int32, device=DEV)
+    ws_bytes = int(lib.sa_prefill_workspace_bytes())
+    ws = torch.zeros(ws_bytes // 4, dtype=torch.int32, device=DEV)
     outs = []
     for w in (ws, None, ws, ws):
         o = torch.empty_like(q)
@@ -171,11 +172,11 @@ def test_persistent_and_grid_launches_agree_and_reset_workspace():
                             v.data_ptr(), *v.stride()[:3], o.data_ptr(), *o.stride()[:3],
                             pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0), None, 0,
                             Hkv, offsets.size(1) - 1, B, Hq, Hkv, T, T, D, bs, 0, 1.0 / math.sqrt(D),
-                            w.data_ptr() if w is not None else None, 8 if w is not None else 0,
+                            w.data_ptr() if w is not None else None, ws_bytes if w is not None else 0,
                             torch.cuda.current_stream().cuda_stream)
         assert st == 0, lib.sa_last_error()
         torch.cuda.synchronize()
-        assert ws.tolist() == [0, 0]
+        assert ws.tolist() == [0] * (ws_bytes // 4)
         outs.append(o)
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
