@@ -804,7 +804,10 @@ struct Prefill {
       return mx * c;
     };
 
-    while (t_cur < n_tiles) {
+    // One step on the tile whose scores are in Sc, filling Sx with the next tile's.  The loop
+    // runs two steps per iteration with the two score sets trading roles, so they are never
+    // copied.
+    auto step = [&](f32x16 (&Sc)[2], f32x16 (&Sx)[2]) {
       const int kb_nxt = kb_cur ^ 1;
       const int vb_prev = vb_cur == 0 ? 2 : vb_cur - 1;
       const int vb_nxt = vb_cur == 2 ? 0 : vb_cur + 1;
@@ -815,7 +818,7 @@ struct Prefill {
       if (t_nxt < n_tiles) dma<false>(it.vb, a.v_st, dl.v, sV + vb_nxt * TILE_BYTES, kt_nxt, a.Tk, wave, lane);
 
       // Upper half: B of the previous tile; the row max it reduces is this tile's.
-      if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, S);
+      if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, Sc);
 
       const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
       const char* cK = sK + kb_nxt * TILE_BYTES;
@@ -831,7 +834,8 @@ struct Prefill {
       auto kfr = [&](int i) { return kfrag(cK, f, i & 1, i >> 1); };
       u32x4 kf[3] = {kfr(0), kfr(1), kfr(2)};
       u32x4 qv[2] = {qfrag(sQw, lane, 0), qfrag(sQw, lane, 1)};
-      f32x16 Sn[2] = {f32x16{}, f32x16{}};
+      Sx[0] = f32x16{};
+      Sx[1] = f32x16{};
       float ls = 0.f;
       uint32_t pw[2][2][4];
       // Raising the priority of the wave in the VALU-heavy block A lets its exponentials go
@@ -840,15 +844,15 @@ struct Prefill {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
-        Sn[i & 1] = E::mfma32(kf[i % 3], qv[(i >> 1) & 1], Sn[i & 1]);
+        Sx[i & 1] = E::mfma32(kf[i % 3], qv[(i >> 1) & 1], Sx[i & 1]);
         if (i + 3 < NQ) kf[i % 3] = kfr(i + 3);
         if ((i & 1) && (i >> 1) + 2 < D / 16) qv[(i >> 1) & 1] = qfrag(sQw, lane, (i >> 1) + 2);
 #pragma unroll
         for (int u = 0; u < PE; u += 2) {
           const int x = PE * i + u;
           const int j = x >> 4, rr = x & 15;
-          const float p0 = fast_exp2(fmaf(S[j][rr], c, neg_m));
-          const float p1 = fast_exp2(fmaf(S[j][rr + 1], c, neg_m));
+          const float p0 = fast_exp2(fmaf(Sc[j][rr], c, neg_m));
+          const float p1 = fast_exp2(fmaf(Sc[j][rr + 1], c, neg_m));
           ls += p0 + p1;
           uint32_t w = E::pack2f(p0, p1);
           // Pins the computation here: without it the compiler sinks the exponentials past
@@ -868,15 +872,13 @@ struct Prefill {
       // wave; about one tile in a row's window).
       const int kbase_n = kt_nxt * KT;
       if (kbase_n + KT - 1 > it.q_abs_min || kbase_n + KT > a.Tk || partial_mask(a, m_nxt)) {
-        mask_tile(a, Sn, row_bits(a, m_nxt, it.hf, it.l32), lim0 - kbase_n);
+        mask_tile(a, Sx, row_bits(a, m_nxt, it.hf, it.l32), lim0 - kbase_n);
       }
 
       // Lower half: B of this tile; the row max it reduces is the next tile's.
-      if (!lag) mt_cur = block_b(sV + vb_cur * TILE_BYTES, Sn);
+      if (!lag) mt_cur = block_b(sV + vb_cur * TILE_BYTES, Sx);
       pending = true;
 
-      S[0] = Sn[0];
-      S[1] = Sn[1];
       wait_dma();
       __syncthreads();
       t_cur = t_nxt;
@@ -886,6 +888,12 @@ struct Prefill {
       m_nxt = m_nn;
       kb_cur = kb_nxt;
       vb_cur = vb_nxt;
+    };
+    f32x16 Sn[2];
+    while (t_cur < n_tiles) {
+      step(S, Sn);
+      if (t_cur >= n_tiles) break;
+      step(Sn, S);
     }
     // Upper half: B of the last tile (its V buffer is not reloaded after the last step).
     if (lag && pending) block_b(sV + (vb_cur == 0 ? 2 : vb_cur - 1) * TILE_BYTES, S);
