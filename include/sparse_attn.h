@@ -189,6 +189,48 @@ int sa_decode(int dtype,
 /* Bytes of fp32 workspace sa_decode needs for num_splits > 1 (0 otherwise). */
 int64_t sa_decode_workspace_bytes(int B, int Hq, int D, int num_splits);
 
+/*
+ * Fused elementwise stages of one decode step of a Qwen3 decoder layer, for the
+ * graph-captured end-to-end decode (callers of the attention path, not the
+ * attention itself).  They keep Hugging Face's arithmetic: fp32 inside,
+ * rounding to the element type where Hugging Face rounds.
+ *
+ * sa_rmsnorm replaces Qwen3RMSNorm.forward and the residual add before it
+ * (transformers/models/qwen3/modeling_qwen3.py, Qwen3DecoderLayer.forward):
+ * for each of `rows` rows of n elements, r = residual + x rounded and stored
+ * back into residual when residual is not NULL (else r = x), then
+ * out = weight * round(r * rsqrt(mean(r^2) + eps)), rounded.  n <= 8192.
+ */
+int sa_rmsnorm(int dtype, const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+               const void* weight, void* out, int64_t out_stride, int rows, int n, float eps, void* stream);
+
+/*
+ * q/k RMSNorm, rotary embedding and paged K/V write of one new token per
+ * sequence, from the fused projection row qkv[b] = q heads | k heads | v heads
+ * (Hq + 2 Hkv heads of D = 128).  Replaces the q_norm / k_norm /
+ * apply_rotary_pos_emb / cache update of the reference's attention forward
+ * (sparse_llm/qwen3/integrations/modeling_sparse_qwen3.py:207-234).
+ * *position (device int64) is the token's position p: cos/sin of
+ * inv_freq[i] * p (D/2 fp32 frequencies), rotate_half convention.  Query heads
+ * go to q_out[b, h, :]; key and value heads to the pages of logical block
+ * p / page (block_table, `max_blocks` columns) at slot p % page of pools
+ * holding num_pages pages (strides in elements: page, head, token); a
+ * position past the table or a page outside the pool is not written.
+ */
+int sa_qk_rope_kv(int dtype, const void* qkv, int64_t qkv_stride, const void* q_norm_weight,
+                  const void* k_norm_weight, const float* inv_freq, const int64_t* position,
+                  void* q_out, int64_t q_out_sb, int64_t q_out_sh,
+                  void* k_pages, void* v_pages, int64_t pages_sp, int64_t pages_sh, int64_t pages_st,
+                  const int32_t* block_table, int64_t block_table_stride, int max_blocks, int num_pages,
+                  int B, int Hq, int Hkv, int D, int page, float eps, void* stream);
+
+/*
+ * SwiGLU of Qwen3MLP: out[b, i] = round(round(silu(g)) * u) with g = gate_up[b, i]
+ * and u = gate_up[b, I + i] (the gate and up projections fused into one row).
+ */
+int sa_swiglu(int dtype, const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride,
+              int B, int I, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

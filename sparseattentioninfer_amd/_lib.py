@@ -72,6 +72,15 @@ SIGNATURES = {
         _vp,
     ]),
     "sa_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "sa_rmsnorm": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
+    "sa_qk_rope_kv": (_i32, [
+        _i32, _vp, _i64, _vp, _vp, _vp, _vp,
+        _vp, _i64, _i64,
+        _vp, _vp, _i64, _i64, _i64,
+        _vp, _i64, _i32, _i32,
+        _i32, _i32, _i32, _i32, _i32, _f32, _vp,
+    ]),
+    "sa_swiglu": (_i32, [_i32, _vp, _i64, _vp, _i64, _i32, _i32, _vp]),
 }
 
 

@@ -395,3 +395,76 @@ def prepare_paged_decode(q, k_pages, v_pages, block_table, kv_lens, sel, sel_off
         num_splits, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
         _stream(q3)]
     return PreparedLaunch("sa_decode", args, (q3, k_pages, v_pages, block_table, kv_lens, sel, sel_off, ws), out)
+
+
+# ---- fused stages of a Qwen3 decode step (graph-captured end-to-end decode) ----------------
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, residual: torch.Tensor | None = None,
+            out: torch.Tensor | None = None) -> torch.Tensor:
+    """Qwen3RMSNorm of the rows of ``x [rows, n]`` (fp32 inside, Hugging Face's roundings).
+
+    With ``residual [rows, n]``: ``residual += x`` (rounded, in place) first, and the sum is
+    normalised -- the residual add and the following norm of a decoder layer in one launch.
+    """
+    name = "rmsnorm"
+    _require(x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and x.dtype in _DTYPES, f"{name}: bad x")
+    rows, n = x.shape
+    _require(weight.shape == (n,) and weight.dtype == x.dtype and weight.is_contiguous(), f"{name}: bad weight")
+    if residual is not None:
+        _require(residual.shape == x.shape and residual.dtype == x.dtype and residual.stride(1) == 1,
+                 f"{name}: bad residual")
+    if out is None:
+        out = torch.empty_like(x)
+    _require(out.shape == x.shape and out.dtype == x.dtype and out.stride(1) == 1, f"{name}: bad out")
+    status = _lib.load().sa_rmsnorm(
+        _DTYPES[x.dtype], x.data_ptr(), x.stride(0),
+        residual.data_ptr() if residual is not None else None, residual.stride(0) if residual is not None else 0,
+        weight.data_ptr(), out.data_ptr(), out.stride(0), rows, n, float(eps), _stream(x))
+    _lib.check("sa_rmsnorm", status)
+    return out
+
+
+def qk_rope_kv(qkv: torch.Tensor, q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
+               inv_freq: torch.Tensor, position: torch.Tensor, store, q_out: torch.Tensor, *,
+               num_heads: int, eps: float) -> torch.Tensor:
+    """q/k RMSNorm + rotary embedding of the fused ``qkv [B, (Hq + 2 Hkv) * D]`` row of one new token per
+    sequence; the query heads go to ``q_out [B, Hq, D]``, the key and value heads into the pages of the
+    :class:`~sparseattentioninfer_amd.models.kv_cache.PagedKVStore` at ``position`` (a device int64
+    ``[1]``); the store's page table must already cover that position."""
+    name = "qk_rope_kv"
+    B = qkv.size(0)
+    Hkv, D = store.heads, store.head_dim
+    _require(qkv.is_cuda and qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.dtype in _DTYPES, f"{name}: bad qkv")
+    _require(qkv.size(1) == (num_heads + 2 * Hkv) * D and B == store.batch, f"{name}: qkv width")
+    _require(store.k_pages.dtype == qkv.dtype and store.k_pages.stride(3) == 1, f"{name}: pages")
+    _require(inv_freq.dtype == torch.float32 and inv_freq.numel() == D // 2 and inv_freq.is_contiguous(),
+             f"{name}: inv_freq must be fp32 [D/2]")
+    _require(position.dtype == torch.int64 and position.is_cuda, f"{name}: position must be a device int64")
+    _require(q_out.shape == (B, num_heads, D) and q_out.stride(2) == 1 and q_out.dtype == qkv.dtype,
+             f"{name}: bad q_out")
+    for w in (q_norm_weight, k_norm_weight):
+        _require(w.shape == (D,) and w.dtype == qkv.dtype and w.is_contiguous(), f"{name}: bad norm weight")
+    kp = store.k_pages
+    status = _lib.load().sa_qk_rope_kv(
+        _DTYPES[qkv.dtype], qkv.data_ptr(), qkv.stride(0), q_norm_weight.data_ptr(), k_norm_weight.data_ptr(),
+        inv_freq.data_ptr(), position.data_ptr(), q_out.data_ptr(), q_out.stride(0), q_out.stride(1),
+        kp.data_ptr(), store.v_pages.data_ptr(), kp.stride(0), kp.stride(1), kp.stride(2),
+        store.block_table.data_ptr(), store.block_table.stride(0), store.block_table.size(1), kp.size(0),
+        B, num_heads, Hkv, D, store.page, float(eps), _stream(qkv))
+    _lib.check("sa_qk_rope_kv", status)
+    return q_out
+
+
+def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``silu(gate) * up`` of Qwen3MLP from the fused ``gate_up [B, 2I]`` (gate first)."""
+    name = "swiglu"
+    _require(gate_up.is_cuda and gate_up.dim() == 2 and gate_up.stride(1) == 1 and gate_up.dtype in _DTYPES
+             and gate_up.size(1) % 2 == 0, f"{name}: bad gate_up")
+    B, I = gate_up.size(0), gate_up.size(1) // 2
+    if out is None:
+        out = torch.empty(B, I, dtype=gate_up.dtype, device=gate_up.device)
+    _require(out.shape == (B, I) and out.stride(1) == 1 and out.dtype == gate_up.dtype, f"{name}: bad out")
+    status = _lib.load().sa_swiglu(_DTYPES[gate_up.dtype], gate_up.data_ptr(), gate_up.stride(0), out.data_ptr(),
+                                   out.stride(0), B, I, _stream(gate_up))
+    _lib.check("sa_swiglu", status)
+    return out

@@ -1,0 +1,303 @@
+"""Greedy decode of a Qwen3SparseKernelForCausalLM, one HIP graph replay per generated token.
+
+The eager decode step (Hugging Face's ``Qwen3ForCausalLM.forward`` with
+:class:`~sparseattentioninfer_amd.qwen3.modeling_sparse_qwen3.Qwen3SparseKernelAttention`)
+spends most of its time launching about twenty small kernels per layer from
+Python.  :class:`GraphDecoder` runs the same per-layer computation -- input
+RMSNorm, q/k/v projections, q/k RMSNorm, rotary embedding, paged K/V write,
+the paged sparse decode kernel, output projection, residuals, post-attention
+RMSNorm, SwiGLU MLP, final norm, LM head, greedy argmax -- on the model's own
+modules, captures it once with ``torch.cuda.CUDAGraph`` (a hipGraph on ROCm)
+and replays it for every token.
+
+Everything that changes from token to token lives on the device, so one
+capture serves every step: the position, the token ids, ``kv_lens``, the page
+and slot of the paged write, and each layer's decode block selection.  The
+selection of a decode step depends only on its query block ``qb = pos // page``
+(the reference's decode row, ``sparse_attentions/patterns/bigbird_pattern.py:236,246``);
+the decoder builds it for every ``qb`` the run can reach with the layer's own
+pattern (``pattern.build`` and the backend's schedule, exactly as the eager
+path does per step) and gathers row ``qb`` on the device.
+
+With ``fused=True`` (the default) a layer is nine launches: one GEMM for the
+concatenated q|k|v projection, ``sa_qk_rope_kv`` (q/k RMSNorm, rotary
+embedding, paged K/V write), the paged decode kernel, the output GEMM,
+``sa_rmsnorm`` (residual add + post-attention norm), one GEMM for the
+concatenated gate|up projection, ``sa_swiglu``, the down GEMM and ``sa_rmsnorm``
+(residual add + the next layer's input norm).  ``fused=False`` calls the model's
+own modules instead (Hugging Face's arithmetic op by op, about 66 launches per
+layer).
+
+The graph holds no ``hipMemsetAsync`` node: the argmax over the vocabulary is
+taken in two small stages, so no multi-block reduction needs a zeroed
+semaphore.
+"""
+from __future__ import annotations
+
+import torch
+from transformers.models.qwen3.modeling_qwen3 import apply_rotary_pos_emb
+
+from .. import ops
+from .paged_cache import PagedKVCache
+
+
+def _argmax_rows(x: torch.Tensor, chunk: int) -> torch.Tensor:
+    """Row-wise argmax of ``x [B, V]`` as two single-block reductions (V % chunk == 0)."""
+    B, V = x.shape
+    v1, i1 = x.view(B, V // chunk, chunk).max(dim=2)        # [B, V / chunk]
+    _, i2 = v1.max(dim=1)                                    # [B]
+    return i2 * chunk + i1.gather(1, i2[:, None])[:, 0]
+
+
+def _argmax_chunk(V: int) -> int:
+    for c in (128, 256, 64, 512, 32, 1024, 16):
+        if V % c == 0:
+            return c
+    return 0
+
+
+class _LayerSchedule:
+    """Decode block selections of one layer for query blocks ``qb0 .. qb1`` (device tables)."""
+
+    def __init__(self, attn, store, qb0: int, qb1: int, batch: int, device):
+        page, H, D = store.page, attn.num_heads, attn.head_dim
+        backend = attn.sparse_backend
+        rows, counts = [], []
+        for qb in range(qb0, qb1 + 1):
+            T_k = qb * page + 1
+            q_like = torch.empty(batch, H, 1, 0, device=device)
+            k_like = torch.empty(batch, attn.num_key_value_heads, T_k, 0, device=device)
+            pattern = attn.sparse_pattern.build(q_like, k_like, causal=True)
+            pairs, offsets, bs = backend._schedule(1, T_k, attn.num_key_value_heads, device, pattern)
+            if bs != page:
+                raise ValueError(f"layer {attn.layer_idx}: schedule block {bs} differs from the page {page}")
+            if offsets.size(1) != 2:
+                raise ValueError(f"layer {attn.layer_idx}: decode expects one CSR query block")
+            start = offsets[:, 0].long()
+            cnt = (offsets[:, 1] - offsets[:, 0]).long()
+            # each row's entries from its own start, zero-padded to the row width
+            width = max(1, int(cnt.max().item()))
+            idx = start[:, None] + torch.arange(width, device=pairs.device)[None, :]
+            ok = torch.arange(width, device=pairs.device)[None, :] < cnt[:, None]
+            row = torch.where(ok, pairs.gather(1, idx.clamp(max=pairs.size(1) - 1)), torch.zeros_like(idx))
+            rows.append(row.to(torch.int32))
+            counts.append(cnt.to(torch.int32))
+        R = rows[0].size(0)
+        self.width = max(r.size(1) for r in rows)
+        self.table = torch.zeros(len(rows), R, self.width, dtype=torch.int32, device=device)
+        for i, r in enumerate(rows):
+            self.table[i, :, :r.size(1)] = r
+        self.counts = torch.stack(counts).to(device)              # [n_qb, R]
+        self.sel = torch.zeros(1, R, self.width, dtype=torch.int32, device=device)
+        self.sel_off = torch.zeros(1, R, 2, dtype=torch.int32, device=device)
+        self.rows = R
+        self.num_splits = ops.auto_decode_splits(batch, R, self.width)
+        need = ops.decode_workspace_bytes(batch, H, D, self.num_splits)
+        self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+
+    def select(self, qb_rel: torch.Tensor) -> None:
+        """Copies the selection of query block ``qb0 + qb_rel`` (a device index) into the buffers."""
+        self.sel.copy_(self.table.index_select(0, qb_rel))
+        self.sel_off[:, :, 1].copy_(self.counts.index_select(0, qb_rel))
+
+
+class GraphDecoder:
+    """Greedy decode steps of ``model`` as replays of one captured HIP graph.
+
+    ``cache`` is the :class:`PagedKVCache` the prompt forward filled, ``ids``
+    the ``[B]`` tokens chosen from the prompt (the next inputs) and ``max_len``
+    the longest sequence the run reaches (the stores' pages are taken up to it
+    once, before capture).  Each :meth:`step` decodes one token per sequence and
+    returns the ``[B]`` device tensor of the chosen next tokens (overwritten by
+    the following step).  The first ``warmup`` steps run eagerly (they warm the
+    libraries the capture records); the next one captures the graph and replays
+    it, and every later one replays it.
+    """
+
+    def __init__(self, model, cache: PagedKVCache, ids: torch.Tensor, max_len: int, *, warmup: int = 2,
+                 keep_logits: bool = False, fused: bool = True):
+        self.model = model
+        inner = model.model
+        cfg = model.config
+        self.layers = list(inner.layers)
+        self.stores = [cache.layers[i].store for i in range(len(self.layers))]
+        if any(s is None for s in self.stores):
+            raise ValueError("GraphDecoder needs a PagedKVCache filled by a prompt forward")
+        st0 = self.stores[0]
+        self.B, self.page, self.dev = st0.batch, st0.page, ids.device
+        self.start = st0.seq_len()
+        if max_len > st0.max_blocks * self.page:
+            raise ValueError(f"max_len {max_len} exceeds the cache capacity {st0.max_blocks * self.page}")
+        self.max_len = max_len
+        for s in self.stores:
+            s._grow_all(max_len)
+        self.head_dim = cfg.head_dim
+        V = cfg.vocab_size
+        self.chunk = _argmax_chunk(V)
+        if not self.chunk:
+            raise ValueError(f"vocab {V} has no power-of-two chunk for the two-stage argmax")
+        for layer in self.layers:
+            if not hasattr(layer.self_attn.sparse_backend, "forward_paged"):
+                raise ValueError("GraphDecoder needs a backend with paged decode (hip_block_sparse)")
+        # one selection table per distinct pattern (dense causal layers all share one)
+        qb0, qb1 = self.start // self.page, (max_len - 1) // self.page
+        self.qb0 = qb0
+        sched: dict = {}
+        self.sched = []
+        for layer, store in zip(self.layers, self.stores):
+            attn = layer.self_attn
+            key = "dense" if attn.pattern_name == "dense" else id(attn.sparse_pattern)
+            if key not in sched:
+                sched[key] = _LayerSchedule(attn, store, qb0, qb1, self.B, self.dev)
+            self.sched.append(sched[key])
+        self.uniq_sched = list(sched.values())
+        # device state
+        self.ids = ids.reshape(self.B).to(torch.long).clone()
+        self.pos = torch.full((1,), self.start, dtype=torch.long, device=self.dev)
+        self.graph = None
+        self.warmup = warmup
+        self.steps_done = 0
+        # last step's LM-head output [B, V] (tests); None unless keep_logits
+        self.logits = torch.empty(self.B, V, dtype=model.lm_head.weight.dtype, device=self.dev) \
+            if keep_logits else None
+        self.fused = fused
+        if fused:
+            self._init_fused(cfg)
+
+    @property
+    def position(self) -> int:
+        """Position of the next token to decode (host view)."""
+        return self.start + self.steps_done
+
+    @torch.inference_mode()
+    def _init_fused(self, cfg) -> None:
+        m = self.model.model
+        if getattr(m.rotary_emb, "attention_scaling", 1.0) != 1.0:
+            raise ValueError("fused decode supports the default rotary embedding (attention_scaling 1)")
+        if self.head_dim != 128:
+            raise ValueError("fused decode supports head dim 128")
+        B, dev = self.B, self.dev
+        dt = self.model.lm_head.weight.dtype
+        attn0 = self.layers[0].self_attn
+        self.num_heads = attn0.num_heads
+        self.eps = float(cfg.rms_norm_eps)
+        self.inv_freq = m.rotary_emb.inv_freq.to(device=dev, dtype=torch.float32).contiguous()
+        self.w_qkv, self.w_gu = [], []
+        for layer in self.layers:
+            a, mlp = layer.self_attn, layer.mlp
+            self.w_qkv.append(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).contiguous())
+            self.w_gu.append(torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).contiguous())
+        hidden = cfg.hidden_size
+        H, D = self.num_heads, self.head_dim
+        new = lambda *shape: torch.empty(*shape, dtype=dt, device=dev)  # noqa: E731
+        self.h = new(B, hidden)                      # residual stream
+        self.x = new(B, hidden)                      # normed activations
+        self.a = new(B, hidden)                      # attention / MLP output before the residual add
+        self.qkv = new(B, self.w_qkv[0].size(0))
+        self.q = new(B, H, D)
+        self.att = new(B, H, D)
+        self.gu = new(B, self.w_gu[0].size(0))
+        self.mid = new(B, self.w_gu[0].size(0) // 2)
+        self.lg = new(B, cfg.vocab_size)
+        self.kv_lens = torch.zeros(B, dtype=torch.int32, device=dev)   # shared by every layer's decode
+
+    @torch.inference_mode()
+    def _step_fused(self) -> None:
+        m = self.model.model
+        L = len(self.layers)
+        self.h.copy_(m.embed_tokens(self.ids))
+        ops.rmsnorm(self.h, self.layers[0].input_layernorm.weight, self.eps, out=self.x)
+        qb_rel = torch.div(self.pos, self.page, rounding_mode="floor") - self.qb0
+        self.kv_lens.copy_((self.pos + 1).to(torch.int32).expand(self.B))
+        for s in self.uniq_sched:
+            s.select(qb_rel)
+        B = self.B
+        for i, (layer, store, sched) in enumerate(zip(self.layers, self.stores, self.sched)):
+            attn = layer.self_attn
+            torch.mm(self.x, self.w_qkv[i].t(), out=self.qkv)
+            ops.qk_rope_kv(self.qkv, attn.q_norm.weight, attn.k_norm.weight, self.inv_freq, self.pos, store, self.q,
+                           num_heads=self.num_heads, eps=self.eps)
+            ops.paged_sparse_decode(
+                self.q, store.k_pages, store.v_pages, store.block_table, self.kv_lens,
+                sched.sel.expand(B, sched.rows, sched.width), sched.sel_off.expand(B, sched.rows, 2),
+                num_splits=sched.num_splits, workspace=sched.workspace if sched.num_splits > 1 else None,
+                out=self.att)
+            torch.mm(self.att.view(B, -1), attn.o_proj.weight.t(), out=self.a)
+            ops.rmsnorm(self.a, layer.post_attention_layernorm.weight, self.eps, residual=self.h, out=self.x)
+            torch.mm(self.x, self.w_gu[i].t(), out=self.gu)
+            ops.swiglu(self.gu, out=self.mid)
+            torch.mm(self.mid, layer.mlp.down_proj.weight.t(), out=self.a)
+            nxt = self.layers[i + 1].input_layernorm.weight if i + 1 < L else m.norm.weight
+            ops.rmsnorm(self.a, nxt, self.eps, residual=self.h, out=self.x)
+        torch.mm(self.x, self.model.lm_head.weight.t(), out=self.lg)
+        if self.logits is not None:
+            self.logits.copy_(self.lg)
+        self.ids.copy_(_argmax_rows(self.lg, self.chunk))
+        self.pos.add_(1)
+
+    def _step(self) -> None:
+        if self.fused:
+            self._step_fused()
+        else:
+            self._step_modules()
+
+    @torch.inference_mode()
+    def _step_modules(self) -> None:
+        m = self.model.model
+        B, D, page = self.B, self.head_dim, self.page
+        h = m.embed_tokens(self.ids[:, None])                                   # [B, 1, hidden]
+        cos, sin = m.rotary_emb(h, self.pos.view(1, 1))
+        qb_rel = torch.div(self.pos, page, rounding_mode="floor") - self.qb0    # [1]
+        slot = (self.pos % page).expand(B)                                      # [B]
+        kv_len = (self.pos + 1).to(torch.int32).expand(B)
+        for s in self.uniq_sched:
+            s.select(qb_rel)
+        for layer, store, sched in zip(self.layers, self.stores, self.sched):
+            attn = layer.self_attn
+            res = h
+            x = layer.input_layernorm(h)
+            shape = (B, 1, -1, D)
+            q = attn.q_norm(attn.q_proj(x).view(shape)).transpose(1, 2)
+            k = attn.k_norm(attn.k_proj(x).view(shape)).transpose(1, 2)
+            v = attn.v_proj(x).view(shape).transpose(1, 2)
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+            pg = store.block_table.index_select(1, qb_rel + self.qb0).view(B).long()
+            store.k_pages[pg, :, slot] = k[:, :, 0].to(store.k_pages.dtype)
+            store.v_pages[pg, :, slot] = v[:, :, 0].to(store.v_pages.dtype)
+            store.kv_lens.copy_(kv_len)
+            out = ops.paged_sparse_decode(
+                q.reshape(B, attn.num_heads, D).contiguous(), store.k_pages, store.v_pages, store.block_table,
+                store.kv_lens, sched.sel.expand(B, sched.rows, sched.width), sched.sel_off.expand(B, sched.rows, 2),
+                num_splits=sched.num_splits, workspace=sched.workspace if sched.num_splits > 1 else None)
+            h = res + attn.o_proj(out.reshape(B, 1, -1))
+            res = h
+            h = res + layer.mlp(layer.post_attention_layernorm(h))
+        h = m.norm(h)
+        logits = self.model.lm_head(h[:, -1])                                   # [B, V]
+        if self.logits is not None:
+            self.logits.copy_(logits)
+        self.ids.copy_(_argmax_rows(logits, self.chunk))
+        self.pos.add_(1)
+
+    def step(self) -> torch.Tensor:
+        """Decodes one token per sequence; returns the chosen next tokens."""
+        if self.position >= self.max_len:
+            raise RuntimeError(f"GraphDecoder reached max_len {self.max_len}")
+        if self.steps_done < self.warmup:
+            self._step()
+        else:
+            if self.graph is None:
+                torch.cuda.synchronize(self.dev)
+                self.graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.graph):
+                    self._step()       # recorded, not run
+            self.graph.replay()
+        self.steps_done += 1
+        return self.ids
+
+    def finish(self) -> None:
+        """Brings the stores' lengths up to date (graph replays advance only the device state)."""
+        n = self.position
+        for s in self.stores:
+            s.lens = [n] * s.batch
+            s.kv_lens.fill_(n)

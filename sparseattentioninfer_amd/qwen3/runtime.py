@@ -73,12 +73,15 @@ def _sync(device):
 
 @torch.inference_mode()
 def greedy_generate(model, input_ids: torch.Tensor, steps: int, *, cache: str = "paged",
-                    max_len: int | None = None, shuffle_seed: int | None = None) -> dict:
+                    max_len: int | None = None, shuffle_seed: int | None = None, graph: bool = False) -> dict:
     """Prompt forward (timed: TTFT) then ``steps`` greedy decode forwards (each timed).
 
     ``cache``: ``"paged"`` (:class:`PagedKVCache`, decode reads pages) or
-    ``"dynamic"`` (HF ``DynamicCache``).  Returns the timings, the generated
-    ids ``[B, steps + 1]`` and the last-position logits of the prompt forward.
+    ``"dynamic"`` (HF ``DynamicCache``).  ``graph`` (paged cache only): decode
+    with :class:`~sparseattentioninfer_amd.qwen3.graph_decode.GraphDecoder`, one
+    HIP graph replay per token, instead of the eager Hugging Face forward.
+    Returns the timings, the generated ids ``[B, steps + 1]`` and the
+    last-position logits of the prompt forward.
     """
     B, T = input_ids.shape
     dev = input_ids.device
@@ -100,7 +103,21 @@ def greedy_generate(model, input_ids: torch.Tensor, steps: int, *, cache: str = 
     first_logits = out.logits[:, -1].float()
     tokens = [nxt]
     step_times = []
-    for _ in range(steps):
+    if graph:
+        if cache != "paged":
+            raise ValueError("graph decode needs the paged cache")
+        from .graph_decode import GraphDecoder
+        dec = GraphDecoder(model, pkv, nxt, T + steps)
+        for _ in range(steps):
+            _sync(dev)
+            t0 = time.perf_counter()
+            ids = dec.step()
+            _sync(dev)
+            step_times.append(time.perf_counter() - t0)
+            tokens.append(ids.clone())
+        dec.finish()
+        steps = len(step_times)
+    for _ in range(0 if graph else steps):
         _sync(dev)
         t0 = time.perf_counter()
         out = model(input_ids=nxt[:, None], past_key_values=pkv, use_cache=True, logits_to_keep=1)

@@ -31,6 +31,18 @@ def assert_close_bf16(got: torch.Tensor, want: torch.Tensor, what: str = ""):
     return max_abs, mean_abs
 
 
+def assert_within_ulps(got: torch.Tensor, want: torch.Tensor, ulps: int, what: str = ""):
+    """Every element of ``got`` within ``ulps`` units in the last place of ``want``'s dtype (bf16:
+    2^-7 of the magnitude's power of two), for results whose arithmetic rounds the same way but
+    may order a reduction differently."""
+    g, w = got.float().cpu(), want.float().cpu()
+    mant = {torch.bfloat16: 7, torch.float16: 10}[want.dtype]
+    ulp = torch.exp2(torch.floor(torch.log2(w.abs().clamp_min(1e-30))) - mant)
+    bad = (g - w).abs() > ulps * ulp
+    assert not bad.any(), (f"{what}: {int(bad.sum())} of {w.numel()} elements beyond {ulps} ulp; worst "
+                           f"{((g - w).abs() / ulp).max().item():.1f} ulp")
+
+
 def golden_case(name: str):
     idx = {c["name"]: c for c in json.loads((GOLDEN / "reference_patterns.json").read_text())}
     data = np.load(GOLDEN / "reference_patterns.npz")

@@ -1,0 +1,88 @@
+"""Fused decode-layer kernels (sa_rmsnorm, sa_qk_rope_kv, sa_swiglu) against the Hugging Face Qwen3 modules
+they replace, at the Qwen3-4B sizes (hidden 2560, 32Q/8KV heads of 128, SwiGLU 9728), batch 8.  The
+kernels keep Hugging Face's roundings, so every element must be within one or two bf16 ulps (reductions
+may sum in another order); page writes must land in the right (page, head, slot)."""
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, Qwen3RotaryEmbedding, apply_rotary_pos_emb
+
+from sparseattentioninfer_amd import ops
+from sparseattentioninfer_amd.models.kv_cache import PagedKVStore
+from sparseattentioninfer_amd.qwen3.runtime import qwen3_config
+from tests.helpers import assert_within_ulps
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _rand(*shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(torch.bfloat16).to(DEV)
+
+
+@pytest.mark.parametrize("with_residual", [False, True])
+def test_rmsnorm_matches_qwen3_rmsnorm(with_residual):
+    _say(f"[layer-ops] rmsnorm residual={with_residual}")
+    B, n, eps = 8, 2560, 1e-6
+    norm = Qwen3RMSNorm(n, eps=eps).to(DEV, torch.bfloat16)
+    with torch.no_grad():
+        norm.weight.copy_(_rand(n, seed=1, scale=0.5) + 1)
+    x, res = _rand(B, n, seed=2, scale=3.0), _rand(B, n, seed=3)
+    r = res.clone()
+    out = ops.rmsnorm(x, norm.weight, eps, residual=r if with_residual else None)
+    src = (res + x) if with_residual else x
+    with torch.no_grad():
+        want = norm(src)
+    if with_residual:
+        assert torch.equal(r, res + x)
+    assert_within_ulps(out, want, 1, "rmsnorm")
+
+
+def test_qk_rope_kv_matches_hf_attention_prologue():
+    _say("[layer-ops] qk_rope_kv")
+    cfg = qwen3_config()
+    B, Hq, Hkv, D, page, eps = 8, 32, 8, 128, 64, 1e-6
+    qn, kn = (Qwen3RMSNorm(D, eps=eps).to(DEV, torch.bfloat16) for _ in range(2))
+    with torch.no_grad():
+        qn.weight.copy_(_rand(D, seed=4, scale=0.3) + 1)
+        kn.weight.copy_(_rand(D, seed=5, scale=0.3) + 1)
+    rope = Qwen3RotaryEmbedding(cfg).to(DEV)
+    qkv = _rand(B, (Hq + 2 * Hkv) * D, seed=6, scale=2.0)
+    store = PagedKVStore(B, Hkv, D, 9000, page=page, dtype=torch.bfloat16, device=DEV, shuffle_seed=9)
+    store.k_pages.zero_()
+    store.v_pages.zero_()
+    for p in (0, 63, 64, 8191, 8990):
+        store._grow_all(p + 1)
+        pos = torch.tensor([p], dtype=torch.int64, device=DEV)
+        q_out = torch.empty(B, Hq, D, dtype=torch.bfloat16, device=DEV)
+        ops.qk_rope_kv(qkv, qn.weight, kn.weight, rope.inv_freq.float(), pos, store, q_out, num_heads=Hq, eps=eps)
+        with torch.no_grad():
+            q = qn(qkv[:, :Hq * D].view(B, 1, Hq, D)).transpose(1, 2)
+            k = kn(qkv[:, Hq * D:(Hq + Hkv) * D].view(B, 1, Hkv, D)).transpose(1, 2)
+            v = qkv[:, (Hq + Hkv) * D:].view(B, 1, Hkv, D).transpose(1, 2)
+            cos, sin = rope(qkv.view(B, 1, -1), pos.view(1, 1))
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        assert_within_ulps(q_out, q[:, :, 0], 2, f"q at position {p}")
+        pg = store.block_table[:, p // page].long()
+        assert_within_ulps(store.k_pages[pg, :, p % page], k[:, :, 0], 2, f"k page at position {p}")
+        assert torch.equal(store.v_pages[pg, :, p % page], v[:, :, 0]), f"v page at position {p}"
+    # only the written slots changed
+    written = (store.k_pages != 0).any(dim=-1).sum().item()
+    assert written == 5 * B * Hkv
+
+
+def test_swiglu_matches_silu_times_up():
+    _say("[layer-ops] swiglu")
+    B, I = 8, 9728
+    gu = _rand(B, 2 * I, seed=7, scale=3.0)
+    out = ops.swiglu(gu)
+    want = F.silu(gu[:, :I]) * gu[:, I:]
+    assert_within_ulps(out, want, 1, "swiglu")
