@@ -231,6 +231,15 @@ int sa_qk_rope_kv(int dtype, const void* qkv, int64_t qkv_stride, const void* q_
 int sa_swiglu(int dtype, const void* gate_up, int64_t gate_up_stride, void* out, int64_t out_stride,
               int B, int I, void* stream);
 
+/*
+ * out[m, n] = sum_k x[m, k] * w[n, k] for M <= 8 rows of x (the projections of a
+ * decode step: F.linear of Hugging Face's Qwen3 modules with M = batch), fp32
+ * accumulation, one rounding of each output.  Streams w once; x rows and w rows
+ * 16-byte aligned, K a multiple of 8 and at most 10240.
+ */
+int sa_gemm_skinny(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride, void* out,
+                   int64_t out_stride, int M, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -81,6 +81,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32, _f32, _vp,
     ]),
     "sa_swiglu": (_i32, [_i32, _vp, _i64, _vp, _i64, _i32, _i32, _vp]),
+    "sa_gemm_skinny": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),
 }
 
 

@@ -13,6 +13,8 @@
 //  * sa_swiglu:       act(gate) * up of Qwen3MLP with SiLU.
 // One wave per row (head) or one workgroup per row; positions come from device memory so the
 // launches can be captured in a graph and replayed at every step.
+#include <algorithm>
+
 #include "sa_common.h"
 
 namespace sa {
@@ -224,4 +226,159 @@ extern "C" int sa_swiglu(int dtype, const void* gate_up, int64_t gate_up_stride,
     hipLaunchKernelGGL(swiglu_kernel<false>, grid, block, 0, s, in, gate_up_stride, oe, out_stride, B, I);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : set_error((int)err, "sa_swiglu: launch failed: %s", hipGetErrorString(err));
+}
+
+// ---- skinny GEMM: out[m, n] = sum_k x[m, k] * W[n, k], M <= 8 (decode-step projections) ----
+//
+// Weight-streaming bound (each W element is used M <= 8 times).  A workgroup of 256 threads owns
+// batches of R consecutive rows of W; thread t owns the 16-byte chunks c = t, t + 256, ... of the
+// K dimension and keeps x's matching chunks for every m in registers for the whole kernel, so W
+// is the only operand streamed.  Per batch a thread forms R * 8 partial sums with packed dot
+// products; a butterfly (each step hands half of the values to the partner lane and adds the
+// other half) leaves the wave's sum of value (lane mod R * 8) in each lane, and the four waves'
+// partials of an output are added through LDS.  fp32 accumulation, one rounding of the output.
+namespace sa {
+
+constexpr int SK_THREADS = 256;
+constexpr int SK_M = 8;      // max rows of x
+constexpr int SK_MAXC = 5;   // 16-byte chunks of K per thread: K <= 5 * 256 * 8 = 10240
+
+template <bool BF16, int NC, int R>
+__global__ __launch_bounds__(SK_THREADS) void skinny_gemm_kernel(const elem_t* x, int64_t x_st, const elem_t* w,
+                                                                 int64_t w_st, elem_t* out, int64_t out_st, int M,
+                                                                 int N, int K) {
+  constexpr int V = R * SK_M;                          // partial sums per thread and batch
+  constexpr int LV = V == 64 ? 6 : V == 32 ? 5 : 4;    // log2(V)
+  static_assert(V == 16 || V == 32 || V == 64, "R must be 2, 4 or 8");
+  __shared__ float s_red[SK_THREADS / 64][V];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kc = K / 8;  // 16-byte chunks
+  uint32_t xr[NC][SK_M][4];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) {
+    const int c = tid + j * SK_THREADS;
+#pragma unroll
+    for (int m = 0; m < SK_M; ++m) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (c < kc && m < M) v = *reinterpret_cast<const u32x4*>(x + m * x_st + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xr[j][m][e] = v[e];
+    }
+  }
+  const int nb = (N + R - 1) / R;
+  for (int bt = blockIdx.x; bt < nb; bt += gridDim.x) {
+    const int n0 = bt * R;
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = tid + j * SK_THREADS;
+      u32x4 wv[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        wv[r] = (c < kc && n0 + r < N) ? *reinterpret_cast<const u32x4*>(w + (int64_t)(n0 + r) * w_st + 8 * c)
+                                       : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < SK_M; ++m) {
+          float a = acc[r * SK_M + m];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a = Elem<BF16>::dot2(wv[r][e], xr[j][m][e], a);
+          acc[r * SK_M + m] = a;
+        }
+    }
+    // Butterfly over lane bits LV-1 .. 0: at step s the partner is lane ^ half (half = V >> (s+1));
+    // the lane whose bit is set keeps the upper half of its values.  Afterwards acc[0] holds the sum,
+    // over the lanes that differ only in bits below LV, of value index (lane & (V - 1)).
+#pragma unroll
+    for (int s = 0; s < LV; ++s) {
+      const int half = V >> (s + 1);
+      const bool upper = lane & half;
+#pragma unroll
+      for (int i = 0; i < half; ++i) {
+        const float give = upper ? acc[i] : acc[i + half];
+        const float keep = upper ? acc[i + half] : acc[i];
+        acc[i] = keep + __shfl_xor(give, half, 64);
+      }
+    }
+#pragma unroll
+    for (int b = V; b < 64; b <<= 1) acc[0] += __shfl_xor(acc[0], b, 64);
+    if (lane < V) s_red[wave][lane] = acc[0];
+    __syncthreads();
+    if (tid < V) {
+      const int r = tid / SK_M, m = tid % SK_M;
+      const float v = s_red[0][tid] + s_red[1][tid] + s_red[2][tid] + s_red[3][tid];
+      if (m < M && n0 + r < N) out[m * out_st + n0 + r] = Elem<BF16>::from_f32(v);
+    }
+    __syncthreads();
+  }
+}
+
+static int num_cus_layer() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <bool BF16, int R>
+static void launch_skinny_r(const elem_t* x, int64_t x_st, const elem_t* w, int64_t w_st, elem_t* out,
+                            int64_t out_st, int M, int N, int K, hipStream_t s) {
+  // Every workgroup loads all of x (M * K * 2 bytes) once, so the grid stays small: two
+  // workgroups per CU (measured best against one and four at the Qwen3-4B decode shapes).
+  const int nb = (N + R - 1) / R;
+  const int grid = std::min(nb, 2 * num_cus_layer());
+  const int nc = (K / 8 + SK_THREADS - 1) / SK_THREADS;
+  const dim3 g(grid), b(SK_THREADS);
+  switch (nc) {
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 1, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 2, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 3, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 4, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 5, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+  }
+}
+
+// Rows per batch: 8 when there are enough batches to give every CU several, else 2.
+template <bool BF16>
+static void launch_skinny(const elem_t* x, int64_t x_st, const elem_t* w, int64_t w_st, elem_t* out,
+                          int64_t out_st, int M, int N, int K, hipStream_t s) {
+  if (N >= 8 * 3 * num_cus_layer())
+    launch_skinny_r<BF16, 8>(x, x_st, w, w_st, out, out_st, M, N, K, s);
+  else
+    launch_skinny_r<BF16, 2>(x, x_st, w, w_st, out, out_st, M, N, K, s);
+}
+
+}  // namespace sa
+
+extern "C" int sa_gemm_skinny(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride, void* out,
+                              int64_t out_stride, int M, int N, int K, void* stream) {
+  using namespace sa;
+  clear_error();
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F16)
+    return set_error(SA_E_DTYPE, "sa_gemm_skinny: dtype %d is not bf16 (0) or f16 (1)", dtype);
+  if (M < 0 || M > SK_M || N < 0 || K < 8 || K % 8 || K > SK_MAXC * SK_THREADS * 8)
+    return set_error(SA_E_SHAPE, "sa_gemm_skinny: M=%d (<= %d), N=%d, K=%d (multiple of 8, <= %d)", M, SK_M, N, K,
+                     SK_MAXC * SK_THREADS * 8);
+  if (M == 0 || N == 0) return 0;
+  if (!x || !w || !out) return set_error(SA_E_NULL, "sa_gemm_skinny: NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w)) & 15 || x_stride % 8 || w_stride % 8)
+    return set_error(SA_E_ALIGN, "sa_gemm_skinny: x and W rows must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto xe = static_cast<const elem_t*>(x);
+  auto we = static_cast<const elem_t*>(w);
+  auto oe = static_cast<elem_t*>(out);
+  if (dtype == SA_DTYPE_BF16)
+    launch_skinny<true>(xe, x_stride, we, w_stride, oe, out_stride, M, N, K, s);
+  else
+    launch_skinny<false>(xe, x_stride, we, w_stride, oe, out_stride, M, N, K, s);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : set_error((int)err, "sa_gemm_skinny: launch failed: %s", hipGetErrorString(err));
 }

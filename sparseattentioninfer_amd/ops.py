@@ -468,3 +468,21 @@ def swiglu(gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tens
                                    out.stride(0), B, I, _stream(gate_up))
     _lib.check("sa_swiglu", status)
     return out
+
+
+def gemm_skinny(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``x [M, K] @ w[N, K]^T`` for M <= 8 (a decode step's projections): streams the weights once,
+    fp32 accumulation, one rounding of each output."""
+    name = "gemm_skinny"
+    _require(x.is_cuda and w.is_cuda and x.dim() == 2 and w.dim() == 2 and x.dtype in _DTYPES
+             and w.dtype == x.dtype and x.stride(1) == 1 and w.stride(1) == 1, f"{name}: bad operands")
+    M, K = x.shape
+    N = w.size(0)
+    _require(w.size(1) == K and M <= 8 and K % 8 == 0 and K <= 10240, f"{name}: M={M} (<= 8), K={K}")
+    if out is None:
+        out = torch.empty(M, N, dtype=x.dtype, device=x.device)
+    _require(out.shape == (M, N) and out.stride(1) == 1 and out.dtype == x.dtype, f"{name}: bad out")
+    status = _lib.load().sa_gemm_skinny(_DTYPES[x.dtype], x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                        out.data_ptr(), out.stride(0), M, N, K, _stream(x))
+    _lib.check("sa_gemm_skinny", status)
+    return out

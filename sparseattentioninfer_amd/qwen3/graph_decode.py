@@ -20,7 +20,8 @@ pattern (``pattern.build`` and the backend's schedule, exactly as the eager
 path does per step) and gathers row ``qb`` on the device.
 
 With ``fused=True`` (the default) a layer is nine launches: one GEMM for the
-concatenated q|k|v projection, ``sa_qk_rope_kv`` (q/k RMSNorm, rotary
+concatenated q|k|v projection (``sa_gemm_skinny``, which streams the weights
+once for the batch's few rows), ``sa_qk_rope_kv`` (q/k RMSNorm, rotary
 embedding, paged K/V write), the paged decode kernel, the output GEMM,
 ``sa_rmsnorm`` (residual add + post-attention norm), one GEMM for the
 concatenated gate|up projection, ``sa_swiglu``, the down GEMM and ``sa_rmsnorm``
@@ -212,9 +213,11 @@ class GraphDecoder:
         for s in self.uniq_sched:
             s.select(qb_rel)
         B = self.B
+        # Projections on the skinny GEMM except the down projection (K = intermediate size), where
+        # reloading x in every workgroup costs more than hipBLASLt's kernel at these shapes.
         for i, (layer, store, sched) in enumerate(zip(self.layers, self.stores, self.sched)):
             attn = layer.self_attn
-            torch.mm(self.x, self.w_qkv[i].t(), out=self.qkv)
+            ops.gemm_skinny(self.x, self.w_qkv[i], out=self.qkv)
             ops.qk_rope_kv(self.qkv, attn.q_norm.weight, attn.k_norm.weight, self.inv_freq, self.pos, store, self.q,
                            num_heads=self.num_heads, eps=self.eps)
             ops.paged_sparse_decode(
@@ -222,14 +225,14 @@ class GraphDecoder:
                 sched.sel.expand(B, sched.rows, sched.width), sched.sel_off.expand(B, sched.rows, 2),
                 num_splits=sched.num_splits, workspace=sched.workspace if sched.num_splits > 1 else None,
                 out=self.att)
-            torch.mm(self.att.view(B, -1), attn.o_proj.weight.t(), out=self.a)
+            ops.gemm_skinny(self.att.view(B, -1), attn.o_proj.weight, out=self.a)
             ops.rmsnorm(self.a, layer.post_attention_layernorm.weight, self.eps, residual=self.h, out=self.x)
-            torch.mm(self.x, self.w_gu[i].t(), out=self.gu)
+            ops.gemm_skinny(self.x, self.w_gu[i], out=self.gu)
             ops.swiglu(self.gu, out=self.mid)
             torch.mm(self.mid, layer.mlp.down_proj.weight.t(), out=self.a)
             nxt = self.layers[i + 1].input_layernorm.weight if i + 1 < L else m.norm.weight
             ops.rmsnorm(self.a, nxt, self.eps, residual=self.h, out=self.x)
-        torch.mm(self.x, self.model.lm_head.weight.t(), out=self.lg)
+        ops.gemm_skinny(self.x, self.model.lm_head.weight, out=self.lg)
         if self.logits is not None:
             self.logits.copy_(self.lg)
         self.ids.copy_(_argmax_rows(self.lg, self.chunk))

@@ -86,3 +86,19 @@ def test_swiglu_matches_silu_times_up():
     out = ops.swiglu(gu)
     want = F.silu(gu[:, :I]) * gu[:, I:]
     assert_within_ulps(out, want, 1, "swiglu")
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 6144, 2560), (8, 2560, 4096), (8, 19456, 2560), (8, 2560, 9728),
+                                   (8, 151936, 2560), (3, 100, 2056), (1, 37, 8)])
+def test_skinny_gemm_matches_fp32_product(M, N, K):
+    _say(f"[layer-ops] gemm_skinny M={M} N={N} K={K}")
+    x = _rand(M, K, seed=10 + M)
+    w = _rand(N, K, seed=20 + N % 97, scale=0.05)
+    out = ops.gemm_skinny(x, w).float()
+    want = x.float() @ w.float().t()
+    # one rounding of the output (half an ulp of bf16) plus fp32 summation in another order, which is
+    # bounded by a small multiple of sum_k |x w| (it matters only where the sum nearly cancels)
+    ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp_min(1e-30))) - 7)
+    bound = 0.5 * ulp + 1e-5 * (x.float().abs() @ w.float().abs().t())
+    bad = (out - want).abs() > bound
+    assert not bad.any(), f"{int(bad.sum())} of {out.numel()} outputs beyond the bound"
