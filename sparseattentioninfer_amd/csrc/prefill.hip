@@ -36,6 +36,7 @@
 // With K rows permuted by krow, register r = 8h + e of the 32-key half j of S^T holds
 // key 32j + 16h + 8g + e.
 #include <algorithm>
+#include <type_traits>
 
 #include "sa_common.h"
 
@@ -106,6 +107,21 @@ __device__ __forceinline__ void load_lds16(const void* sbase, uint32_t voff, uin
       : "memory", "m0");
 }
 
+// Uniform base plus per-lane offset plus the immediate IMM (a signed 13-bit field of the
+// instruction), so consecutive loads from one base need no address arithmetic.  The
+// instruction adds IMM to the LDS address as well (M0 + IMM + 16 l), so M0 is lds - IMM.
+template <int IMM>
+__device__ __forceinline__ void load_lds16_at(const void* sbase, uint32_t voff, uint32_t lds) {
+  static_assert(IMM >= -4096 && IMM < 4096, "global instruction offsets are 13-bit signed");
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1 offset:%3"
+      :
+      : "v"(voff), "s"(sbase), "s"(lds - (uint32_t)IMM), "i"(IMM)
+      : "memory", "m0");
+}
+
 // Per-lane 64-bit address.
 __device__ __forceinline__ void load_lds16(const void* vaddr, uint32_t lds) {
   asm volatile(
@@ -134,6 +150,18 @@ __device__ __forceinline__ int32_t load_uniform_now(const int32_t* p) {
       : "v"(p)
       : "memory");
   return __builtin_amdgcn_readfirstlane(x);
+}
+
+// Per-lane 32-bit global read that has completed when it returns (same reason as above).
+__device__ __forceinline__ int32_t load_lane_now(const int32_t* p) {
+  int32_t x;
+  asm volatile(
+      "global_load_dword %0, %1, off\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=v"(x)
+      : "v"(p)
+      : "memory");
+  return x;
 }
 
 // SUB: tile schedules with sub-block masks (block sizes 16 and 32); without it the mask
@@ -389,6 +417,88 @@ struct Prefill {
       if (kt >= 0 && kt * KT < a.Tk && kt * KT <= it.q_abs_tile_max) break;
     }
     return t;
+  }
+
+  // The usable tiles of an item in schedule order, read 64 schedule positions at a time:
+  // lane i of `kt` holds the key tile of position `next - 64 + i` (and lane i of `m` its
+  // sub-block mask), bit i of `live` marks it usable and not yet taken.  A tile is usable
+  // under the rule of next_usable: 0 <= kt <= kt_hi, the last key tile that starts before T_k
+  // and at or before the causal limit of the query tile.
+  struct TileQueue {
+    int kt;
+    uint32_t m;
+    uint64_t live;
+    int next;
+    int kt_hi;
+  };
+
+  static __device__ __forceinline__ TileQueue queue_begin(const PrefillArgs& a, const Item& it) {
+    TileQueue q;
+    q.kt = 0;
+    q.m = 0;
+    q.live = 0;
+    q.next = 0;
+    q.kt_hi = min((a.Tk + KT - 1) / KT - 1, it.q_abs_tile_max / KT);
+    return q;
+  }
+
+  static __device__ __forceinline__ void queue_fill(const PrefillArgs& a, const Item& it, const int32_t* s_row,
+                                                    const int32_t* s_mask, TileQueue& q) {
+    const int t = q.next + (threadIdx.x & 63);
+    int blk = -1;
+    uint32_t m = 0;
+    if (t < it.n_tiles) {
+      const int e = t >> a.tpb_log2;
+      blk = it.cached ? s_row[e] : load_lane_now(it.prow + it.e0 + e);
+      if (SUB) m = (uint32_t)(it.cached ? s_mask[e] : load_lane_now(it.mrow + it.e0 + e));
+    }
+    // Block ids past kt_hi's block are rejected before the product, which cannot overflow then.
+    const bool ok = blk >= 0 && blk <= (q.kt_hi >> a.tpb_log2);
+    q.kt = ok ? blk * (1 << a.tpb_log2) + (t & it.tpb_mask) : -1;
+    q.m = m;
+    q.live = __builtin_amdgcn_ballot_w64(ok && q.kt <= q.kt_hi);
+    q.next += 64;
+  }
+
+  // Takes the next usable tile (key tile kt, sub-block mask m); false when none is left.
+  static __device__ __forceinline__ bool queue_pop(const PrefillArgs& a, const Item& it, const int32_t* s_row,
+                                                   const int32_t* s_mask, TileQueue& q, int& kt, uint32_t& m) {
+    while (q.live == 0) {
+      if (q.next >= it.n_tiles) return false;
+      queue_fill(a, it, s_row, s_mask, q);
+    }
+    const int l = __builtin_ctzll(q.live);
+    q.live &= q.live - 1;
+    kt = __builtin_amdgcn_readlane(q.kt, l);
+    if (SUB) m = (uint32_t)__builtin_amdgcn_readlane((int)q.m, l);
+    return true;
+  }
+
+  // Source of this wave's direct loads for key tile 0 of K or V (uniform) and the bytes per
+  // key tile; the wave's NIW loads of a tile share one row block (NIW <= NCG).
+  struct Src {
+    const char* p;
+    uint32_t tile_bytes;
+  };
+  static __device__ __forceinline__ Src src_of(const elem_t* base, int64_t st, int wave) {
+    const int k0 = wave * NIW;
+    return {reinterpret_cast<const char*>(base) + ((int64_t)16 * (k0 / NCG) * st + 32 * (k0 % NCG)) * 2,
+            (uint32_t)(KT * st * 2)};
+  }
+
+  // LDS address of this wave's share of a staged tile.
+  static __device__ __forceinline__ uint32_t dma_lds(const char* tile, int wave) {
+    const int k0 = wave * NIW;
+    return lds_addr(tile + (k0 % NCG) * 4096 + (k0 / NCG) * 1024);
+  }
+
+  // dma() for a key tile wholly before T_k: one 64-bit product for the tile's address, the
+  // column groups 64 bytes apart in the load instructions' offsets.
+  static __device__ __forceinline__ void dma_full(const Src& s, uint32_t off, uint32_t lds, int kt) {
+    static_assert(NIW <= NCG && NIW <= 2, "one row block, at most two loads per wave");
+    const char* wb = s.p + (uint64_t)(uint32_t)kt * s.tile_bytes;
+    load_lds16_at<0>(wb, off, lds);
+    if constexpr (NIW > 1) load_lds16_at<64>(wb, off, lds + 4096);
   }
 
   // O / l written through this wave's 32 x D staging area in LDS (rows at 2D bytes, 16-byte
@@ -728,21 +838,39 @@ struct Prefill {
     float m_ref = -__builtin_inff();
     float l_run = 0.f;
     const float c = a.scale_log2;
-    const int n_tiles = it.n_tiles;
 
-    // Prime: K of tiles t0, t1 in K buffers 0, 1 and V of t0 in V buffer 0; S^T and row
-    // max of t0.
-    int t_cur = next_usable(a, it, s_row, 0);
-    int t_nxt = t_cur < n_tiles ? next_usable(a, it, s_row, t_cur + 1) : n_tiles;
-    int kt_cur = t_cur < n_tiles ? tile_of(a, it, s_row, t_cur) : 0;
-    int kt_nxt = t_nxt < n_tiles ? tile_of(a, it, s_row, t_nxt) : 0;
-    const uint32_t m_cur = sub_log2(a) && t_cur < n_tiles ? mask_of(it, s_mask, t_cur) : 0u;
-    uint32_t m_nxt = sub_log2(a) && t_nxt < n_tiles ? mask_of(it, s_mask, t_nxt) : 0u;
-    if (t_cur < n_tiles) {
-      dma<true>(it.kb, a.k_st, dl.k, sK, kt_cur, a.Tk, wave, lane);
-      dma<false>(it.vb, a.v_st, dl.v, sV, kt_cur, a.Tk, wave, lane);
+    // Direct loads of key tile kt into K buffer kb / V buffer vb (full tiles from one uniform
+    // address per load, the tile at T_k row by row).
+    const Src src_k = src_of(it.kb, a.k_st, wave);
+    const Src src_v = src_of(it.vb, a.v_st, wave);
+    const uint32_t lds_k = dma_lds(sK, wave);
+    const uint32_t lds_v = dma_lds(sV, wave);
+    const int kt_full = a.Tk / KT;  // key tiles wholly before T_k
+    auto load_k = [&](int kt, int kb) {
+      if (kt < kt_full)
+        dma_full(src_k, dl.k, lds_k + kb * TILE_BYTES, kt);
+      else
+        dma<true>(it.kb, a.k_st, dl.k, sK + kb * TILE_BYTES, kt, a.Tk, wave, lane);
+    };
+    auto load_v = [&](int kt, int vb) {
+      if (kt < kt_full)
+        dma_full(src_v, dl.v, lds_v + vb * TILE_BYTES, kt);
+      else
+        dma<false>(it.vb, a.v_st, dl.v, sV + vb * TILE_BYTES, kt, a.Tk, wave, lane);
+    };
+
+    // Prime: K of the first two usable tiles in K buffers 0, 1 and V of the first in V
+    // buffer 0; S^T and row max of the first.
+    TileQueue q = queue_begin(a, it);
+    int kt_cur = 0, kt_nxt = 0;
+    uint32_t m_cur = 0u, m_nxt = 0u;
+    bool has_cur = queue_pop(a, it, s_row, s_mask, q, kt_cur, m_cur);
+    bool has_nxt = has_cur && queue_pop(a, it, s_row, s_mask, q, kt_nxt, m_nxt);
+    if (has_cur) {
+      load_k(kt_cur, 0);
+      load_v(kt_cur, 0);
     }
-    if (t_nxt < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+    if (has_nxt) load_k(kt_nxt, 1);
     LookLoads ld;
     if constexpr (LOOK) look_issue(a, *lk, ld);
     wait_dma();
@@ -750,7 +878,7 @@ struct Prefill {
     __syncthreads();
     f32x16 S[2] = {f32x16{}, f32x16{}};  // scores of the current tile
     float mt_cur = -__builtin_inff();
-    if (t_cur < n_tiles) {
+    if (has_cur) {
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
         const u32x4 qv = qfrag(sQw, lane, cc);
@@ -770,7 +898,6 @@ struct Prefill {
     // in step i by both halves, K of tile i+2 loads); V is triple-buffered (V of tiles i-1
     // and i are read, V of tile i+1 loads), so one barrier per step still suffices.
     const bool lag = it.hf == 1;  // upper half: one half-step behind
-    int kb_cur = 0;  // K buffer of the current tile (the next tile's is kb_cur ^ 1)
     int vb_cur = 0;  // V buffer of the current tile (tile i in buffer i mod 3)
     bool pending = false;  // upper half: B of the previous tile still to run
     u32x4 P[2][2];         // probabilities of the tile whose B is next
@@ -804,18 +931,19 @@ struct Prefill {
       return mx * c;
     };
 
-    // One step on the tile whose scores are in Sc, filling Sx with the next tile's.  The loop
-    // runs two steps per iteration with the two score sets trading roles, so they are never
-    // copied.
-    auto step = [&](f32x16 (&Sc)[2], f32x16 (&Sx)[2]) {
-      const int kb_nxt = kb_cur ^ 1;
+    // One step on the tile whose scores are in Sc and whose K is in buffer KB, filling Sx
+    // with the next tile's.  The loop runs two steps per iteration with the two score sets
+    // and K buffers trading roles, so scores are never copied and K buffers are constants.
+    auto step = [&](auto kb_tag, f32x16 (&Sc)[2], f32x16 (&Sx)[2]) {
+      constexpr int kb_cur = decltype(kb_tag)::value;
+      constexpr int kb_nxt = kb_cur ^ 1;
       const int vb_prev = vb_cur == 0 ? 2 : vb_cur - 1;
       const int vb_nxt = vb_cur == 2 ? 0 : vb_cur + 1;
-      const int t_nn = t_nxt < n_tiles ? next_usable(a, it, s_row, t_nxt + 1) : n_tiles;
-      const int kt_nn = t_nn < n_tiles ? tile_of(a, it, s_row, t_nn) : 0;
-      const uint32_t m_nn = sub_log2(a) && t_nn < n_tiles ? mask_of(it, s_mask, t_nn) : 0u;
-      if (t_nn < n_tiles) dma<true>(it.kb, a.k_st, dl.k, sK + kb_cur * TILE_BYTES, kt_nn, a.Tk, wave, lane);
-      if (t_nxt < n_tiles) dma<false>(it.vb, a.v_st, dl.v, sV + vb_nxt * TILE_BYTES, kt_nxt, a.Tk, wave, lane);
+      int kt_nn = 0;
+      uint32_t m_nn = 0u;
+      const bool has_nn = has_nxt && queue_pop(a, it, s_row, s_mask, q, kt_nn, m_nn);
+      if (has_nn) load_k(kt_nn, kb_cur);
+      if (has_nxt) load_v(kt_nxt, vb_nxt);
 
       // Upper half: B of the previous tile; the row max it reduces is this tile's.
       if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, Sc);
@@ -881,19 +1009,18 @@ struct Prefill {
 
       wait_dma();
       __syncthreads();
-      t_cur = t_nxt;
+      has_cur = has_nxt;
       kt_cur = kt_nxt;
-      t_nxt = t_nn;
+      has_nxt = has_nn;
       kt_nxt = kt_nn;
       m_nxt = m_nn;
-      kb_cur = kb_nxt;
       vb_cur = vb_nxt;
     };
     f32x16 Sn[2];
-    while (t_cur < n_tiles) {
-      step(S, Sn);
-      if (t_cur >= n_tiles) break;
-      step(Sn, S);
+    while (has_cur) {
+      step(std::integral_constant<int, 0>{}, S, Sn);
+      if (!has_cur) break;
+      step(std::integral_constant<int, 1>{}, Sn, S);
     }
     // Upper half: B of the last tile (its V buffer is not reloaded after the last step).
     if (lag && pending) block_b(sV + (vb_cur == 0 ? 2 : vb_cur - 1) * TILE_BYTES, S);

@@ -182,3 +182,53 @@ def test_persistent_and_grid_launches_agree_and_reset_workspace():
         assert torch.equal(o, outs[0])
     want = oa.block_sparse_attention(q, k, v, pairs.cpu(), offsets.cpu(), bs)
     assert_close_bf16(outs[0], want, "persistent")
+
+
+def _csr(rows):
+    """CSR (pairs [R, width], offsets [R, nqb + 1]) from per-row lists of key-block lists."""
+    width = max(1, max(sum(len(e) for e in r) for r in rows))
+    pairs = torch.full((len(rows), width), -7, dtype=torch.int32)
+    offsets = torch.zeros(len(rows), len(rows[0]) + 1, dtype=torch.int32)
+    for r, blocks in enumerate(rows):
+        flat = [b for e in blocks for b in e]
+        pairs[r, :len(flat)] = torch.tensor(flat, dtype=torch.int32)
+        offsets[r, 1:] = torch.tensor(np.cumsum([len(e) for e in blocks]), dtype=torch.int32)
+    return pairs, offsets
+
+
+@pytest.mark.parametrize("bs", [64, 128])
+def test_long_rows_with_unusable_entries(bs):
+    """Four-head (pipelined) workgroups over rows of hundreds to over a thousand entries: schedule
+    positions are read 64 at a time, rows past the 1,024-entry LDS cache from global memory, and
+    entries the kernel skips fall anywhere in a row, including on 64-position boundaries.  Blocks
+    wholly after the query tile's causal limit are checked against the oracle (which masks them);
+    blocks past T_k and negative ids, which the oracle cannot take, must leave the bits of the
+    result unchanged."""
+    B, Hq, Hkv, D = 1, 4, 1, 128
+    T_q, T_k = 2 * bs, (70000 if bs == 64 else 40000)
+    nkb, nqb = -(-T_k // bs), 2
+    _say(f"[prefill] long rows bs={bs} T_k={T_k}")
+    rng = np.random.default_rng(bs)
+    clean, junk = [], []
+    for qb in range(nqb):
+        if qb == 0:
+            blocks = list(range(nkb))  # every key block: the last ones lie after the causal limit
+            for pos in (63, 64, 128, 129):  # more of those, on window boundaries
+                blocks.insert(pos, nkb - 1)
+        else:
+            blocks = sorted(rng.choice(nkb, size=min(600, nkb // 2), replace=False).tolist())
+        bad = list(blocks)
+        for pos, blk in ((0, -1), (63, nkb), (64, -1), (65, nkb + 3), (127, -2), (300, nkb + 1), (len(bad), -1)):
+            bad.insert(min(pos, len(bad)), blk)
+        clean.append(blocks)
+        junk.append(bad)
+    assert len(clean[0]) > 1024 or bs == 128
+    pairs, offsets = _csr([clean])
+    pairs_j, offsets_j = _csr([junk])
+    q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T_q, T_k, D, torch.bfloat16, seed=21))
+    out = ops.universal_sparse_attn(q, k, v, pairs.to(DEV), offsets.to(DEV), bs)
+    out_j = ops.universal_sparse_attn(q, k, v, pairs_j.to(DEV), offsets_j.to(DEV), bs)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_j), "skipped entries changed the result"
+    want = oa.block_sparse_attention(q, k, v, pairs, offsets, bs)
+    assert_close_bf16(out, want, f"long rows bs={bs}")
