@@ -51,6 +51,8 @@ CASES = [
     ("fp16_group", 1, 8, 2, 640, 640, 128, 64, "bernoulli0.2", "kv", torch.float16),
     ("chunk_tail", 1, 4, 2, 200, 1000, 128, 64, "bernoulli0.3", "kv", torch.bfloat16),
     ("cfg2_slice", 1, 32, 8, 2048, 2048, 128, 64, "bernoulli0.1", "kv", torch.bfloat16),
+    ("d64_group_ragged", 2, 8, 2, 1000, 1000, 64, 64, "bernoulli0.3", "kv", torch.bfloat16),
+    ("d64_block128_fp16", 1, 8, 2, 900, 900, 64, 128, "bernoulli0.4", "kv", torch.float16),
 ]
 
 
