@@ -31,8 +31,8 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-constexpr int NORM_THREADS = 256;
-constexpr int NORM_MAX_PER_THREAD = 32;  // hidden sizes up to 8192
+constexpr int NORM_THREADS = 1024;
+constexpr int NORM_MAX_PER_THREAD = 8;  // hidden sizes up to 8192
 
 // One workgroup per row: r = residual + x (rounded; stored back) when residual is given,
 // else r = x; out = w * rnd(r * rsqrt(mean(r^2) + eps)) rounded.
@@ -45,20 +45,36 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(const elem_t* x, 
   const int tid = threadIdx.x;
   const elem_t* xr = x + row * x_st;
   elem_t* rr = res ? res + row * res_st : nullptr;
-  float v[NORM_MAX_PER_THREAD];
+  // Every load of the row (x, residual, weight) is issued before the first store: the stores
+  // may alias the inputs as far as the compiler knows, so interleaving them would serialise
+  // the row into one memory round trip per element slot.
+  float xv[NORM_MAX_PER_THREAD], rv[NORM_MAX_PER_THREAD], wv[NORM_MAX_PER_THREAD];
+#pragma unroll
+  for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
+    const int i = tid + u * NORM_THREADS;
+    xv[u] = rv[u] = wv[u] = 0.f;
+    if (i < n) {
+      xv[u] = ld<BF16>(xr + i);
+      if (rr) rv[u] = ld<BF16>(rr + i);
+      wv[u] = ld<BF16>(w + i);
+    }
+  }
   float ss = 0.f;
 #pragma unroll
   for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
     const int i = tid + u * NORM_THREADS;
-    v[u] = 0.f;
     if (i < n) {
-      float r = ld<BF16>(xr + i);
-      if (rr) {
-        r = rnd<BF16>(ld<BF16>(rr + i) + r);
-        rr[i] = Elem<BF16>::from_f32(r);
-      }
-      v[u] = r;
+      float r = xv[u];
+      if (rr) r = rnd<BF16>(rv[u] + r);
+      xv[u] = r;
       ss += r * r;
+    }
+  }
+  if (rr) {
+#pragma unroll
+    for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
+      const int i = tid + u * NORM_THREADS;
+      if (i < n) rr[i] = Elem<BF16>::from_f32(xv[u]);
     }
   }
   ss = wave_sum(ss);
@@ -72,7 +88,7 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(const elem_t* x, 
 #pragma unroll
   for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
     const int i = tid + u * NORM_THREADS;
-    if (i < n) orow[i] = Elem<BF16>::from_f32(ld<BF16>(w + i) * rnd<BF16>(v[u] * inv));
+    if (i < n) orow[i] = Elem<BF16>::from_f32(wv[u] * rnd<BF16>(xv[u] * inv));
   }
 }
 
@@ -139,6 +155,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const elem_t* gu, int64_t g
   const float a = rnd<BF16>(g / (1.f + expf(-g)));
   out[b * out_st + i] = Elem<BF16>::from_f32(a * u);
 }
+
 
 }  // namespace sa
 
@@ -233,8 +250,10 @@ extern "C" int sa_swiglu(int dtype, const void* gate_up, int64_t gate_up_stride,
 // Weight-streaming bound (each W element is used M <= 8 times).  A workgroup of 256 threads owns
 // batches of R consecutive rows of W; thread t owns the 16-byte chunks c = t, t + 256, ... of the
 // K dimension and keeps x's matching chunks for every m in registers for the whole kernel, so W
-// is the only operand streamed.  Per batch a thread forms R * 8 partial sums with packed dot
-// products; a butterfly (each step hands half of the values to the partner lane and adds the
+// is the only operand streamed.  A thread issues all its loads of a batch's W rows at once, and
+// for R <= 4 with K in at most two chunks per thread the next batch's rows load while the
+// current batch is multiplied and reduced.  Per batch a thread forms R * 8 partial sums with
+// packed dot products; a butterfly (each step hands half of the values to the partner lane and adds the
 // other half) leaves the wave's sum of value (lane mod R * 8) in each lane, and the four waves'
 // partials of an output are added through LDS.  fp32 accumulation, one rounding of the output.
 namespace sa {
@@ -243,7 +262,7 @@ constexpr int SK_THREADS = 256;
 constexpr int SK_M = 8;      // max rows of x
 constexpr int SK_MAXC = 5;   // 16-byte chunks of K per thread: K <= 5 * 256 * 8 = 10240
 
-template <bool BF16, int NC, int R>
+template <bool BF16, int NC, int R, bool PF>
 __global__ __launch_bounds__(SK_THREADS) void skinny_gemm_kernel(const elem_t* x, int64_t x_st, const elem_t* w,
                                                                  int64_t w_st, elem_t* out, int64_t out_st, int M,
                                                                  int N, int K) {
@@ -266,29 +285,36 @@ __global__ __launch_bounds__(SK_THREADS) void skinny_gemm_kernel(const elem_t* x
     }
   }
   const int nb = (N + R - 1) / R;
-  for (int bt = blockIdx.x; bt < nb; bt += gridDim.x) {
+  // This thread's NC chunks of the R rows of W in batch bt (zeros past the end).
+  auto load_w = [&](int bt, u32x4 (&wv)[NC][R]) {
+#pragma unroll
+    for (int j = 0; j < NC; ++j) {
+      const int c = tid + j * SK_THREADS;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int n = bt * R + r;
+        wv[j][r] = (bt < nb && c < kc && n < N) ? *reinterpret_cast<const u32x4*>(w + (int64_t)n * w_st + 8 * c)
+                                                : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  // Dot products, reduction over the workgroup and store of batch bt.
+  auto batch = [&](int bt, const u32x4 (&wv)[NC][R]) {
     const int n0 = bt * R;
     float acc[V];
 #pragma unroll
     for (int i = 0; i < V; ++i) acc[i] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NC; ++j) {
-      const int c = tid + j * SK_THREADS;
-      u32x4 wv[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        wv[r] = (c < kc && n0 + r < N) ? *reinterpret_cast<const u32x4*>(w + (int64_t)(n0 + r) * w_st + 8 * c)
-                                       : u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < NC; ++j)
 #pragma unroll
       for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int m = 0; m < SK_M; ++m) {
           float a = acc[r * SK_M + m];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a = Elem<BF16>::dot2(wv[r][e], xr[j][m][e], a);
+          for (int e = 0; e < 4; ++e) a = Elem<BF16>::dot2(wv[j][r][e], xr[j][m][e], a);
           acc[r * SK_M + m] = a;
         }
-    }
     // Butterfly over lane bits LV-1 .. 0: at step s the partner is lane ^ half (half = V >> (s+1));
     // the lane whose bit is set keeps the upper half of its values.  Afterwards acc[0] holds the sum,
     // over the lanes that differ only in bits below LV, of value index (lane & (V - 1)).
@@ -313,6 +339,28 @@ __global__ __launch_bounds__(SK_THREADS) void skinny_gemm_kernel(const elem_t* x
       if (m < M && n0 + r < N) out[m * out_st + n0 + r] = Elem<BF16>::from_f32(v);
     }
     __syncthreads();
+  };
+  if constexpr (PF) {
+    // The next batch's rows load while this one is multiplied and reduced; two register sets
+    // trade roles, so nothing is copied.
+    u32x4 wa[NC][R], wb[NC][R];
+    int bt = blockIdx.x;
+    load_w(bt, wa);
+    while (bt < nb) {
+      load_w(bt + gridDim.x, wb);
+      batch(bt, wa);
+      bt += gridDim.x;
+      if (bt >= nb) break;
+      load_w(bt + gridDim.x, wa);
+      batch(bt, wb);
+      bt += gridDim.x;
+    }
+  } else {
+    for (int bt = blockIdx.x; bt < nb; bt += gridDim.x) {
+      u32x4 wv[NC][R];
+      load_w(bt, wv);
+      batch(bt, wv);
+    }
   }
 }
 
@@ -330,30 +378,32 @@ static int num_cus_layer() {
 
 template <bool BF16, int R>
 static void launch_skinny_r(const elem_t* x, int64_t x_st, const elem_t* w, int64_t w_st, elem_t* out,
-                            int64_t out_st, int M, int N, int K, hipStream_t s) {
-  // Every workgroup loads all of x (M * K * 2 bytes) once, so the grid stays small: two
-  // workgroups per CU (measured best against one and four at the Qwen3-4B decode shapes).
+                            int64_t out_st, int M, int N, int K, int per_cu, hipStream_t s) {
   const int nb = (N + R - 1) / R;
-  const int grid = std::min(nb, 2 * num_cus_layer());
+  const int grid = std::min(nb, per_cu * num_cus_layer());
   const int nc = (K / 8 + SK_THREADS - 1) / SK_THREADS;
   const dim3 g(grid), b(SK_THREADS);
+  constexpr bool PF = R <= 4;  // registers for two sets of W chunks when NC <= 2
   switch (nc) {
-    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 1, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
-    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 2, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
-    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 3, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
-    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 4, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
-    default: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 5, R>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 1: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 1, R, PF>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 2: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 2, R, PF>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 3: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 3, R, false>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    case 4: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 4, R, false>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
+    default: hipLaunchKernelGGL((skinny_gemm_kernel<BF16, 5, R, false>), g, b, 0, s, x, x_st, w, w_st, out, out_st, M, N, K); break;
   }
 }
 
-// Rows per batch: 8 when there are enough batches to give every CU several, else 2.
+// Rows per batch and workgroups per CU, measured at the Qwen3-4B decode shapes with the weights
+// streamed from HBM: wide products (N >= 64 per CU: gate|up, LM head) take 4 rows per batch and
+// three workgroups per CU; the others 2 rows, with four workgroups per CU while K fits two
+// chunks per thread (q|k|v, o) and two past that (down, where each workgroup's x is large).
 template <bool BF16>
 static void launch_skinny(const elem_t* x, int64_t x_st, const elem_t* w, int64_t w_st, elem_t* out,
                           int64_t out_st, int M, int N, int K, hipStream_t s) {
-  if (N >= 8 * 3 * num_cus_layer())
-    launch_skinny_r<BF16, 8>(x, x_st, w, w_st, out, out_st, M, N, K, s);
+  if (N >= 64 * num_cus_layer())
+    launch_skinny_r<BF16, 4>(x, x_st, w, w_st, out, out_st, M, N, K, 3, s);
   else
-    launch_skinny_r<BF16, 2>(x, x_st, w, w_st, out, out_st, M, N, K, s);
+    launch_skinny_r<BF16, 2>(x, x_st, w, w_st, out, out_st, M, N, K, K > 2 * SK_THREADS * 8 ? 2 : 4, s);
 }
 
 }  // namespace sa

@@ -199,6 +199,8 @@ class GraphDecoder:
         self.att = new(B, H, D)
         self.gu = new(B, self.w_gu[0].size(0))
         self.mid = new(B, self.w_gu[0].size(0) // 2)
+        inter = self.mid.size(1)
+        self.down_skinny = inter % 8 == 0 and inter <= 10240  # sa_gemm_skinny's K limit
         self.lg = new(B, cfg.vocab_size)
         self.kv_lens = torch.zeros(B, dtype=torch.int32, device=dev)   # shared by every layer's decode
 
@@ -213,8 +215,8 @@ class GraphDecoder:
         for s in self.uniq_sched:
             s.select(qb_rel)
         B = self.B
-        # Projections on the skinny GEMM except the down projection (K = intermediate size), where
-        # reloading x in every workgroup costs more than hipBLASLt's kernel at these shapes.
+        # Every projection on the skinny GEMM (the down projection on hipBLASLt when its K, the
+        # intermediate size, is past the skinny kernel's limit).
         for i, (layer, store, sched) in enumerate(zip(self.layers, self.stores, self.sched)):
             attn = layer.self_attn
             ops.gemm_skinny(self.x, self.w_qkv[i], out=self.qkv)
@@ -229,7 +231,10 @@ class GraphDecoder:
             ops.rmsnorm(self.a, layer.post_attention_layernorm.weight, self.eps, residual=self.h, out=self.x)
             ops.gemm_skinny(self.x, self.w_gu[i], out=self.gu)
             ops.swiglu(self.gu, out=self.mid)
-            torch.mm(self.mid, layer.mlp.down_proj.weight.t(), out=self.a)
+            if self.down_skinny:
+                ops.gemm_skinny(self.mid, layer.mlp.down_proj.weight, out=self.a)
+            else:
+                torch.mm(self.mid, layer.mlp.down_proj.weight.t(), out=self.a)
             nxt = self.layers[i + 1].input_layernorm.weight if i + 1 < L else m.norm.weight
             ops.rmsnorm(self.a, nxt, self.eps, residual=self.h, out=self.x)
         ops.gemm_skinny(self.x, self.model.lm_head.weight, out=self.lg)

@@ -31,13 +31,15 @@ def assert_close_bf16(got: torch.Tensor, want: torch.Tensor, what: str = ""):
     return max_abs, mean_abs
 
 
-def assert_within_ulps(got: torch.Tensor, want: torch.Tensor, ulps: int, what: str = ""):
+def assert_within_ulps(got: torch.Tensor, want: torch.Tensor, ulps: int, what: str = "", scale: float = 0.0):
     """Every element of ``got`` within ``ulps`` units in the last place of ``want``'s dtype (bf16:
     2^-7 of the magnitude's power of two), for results whose arithmetic rounds the same way but
-    may order a reduction differently."""
+    may order a reduction differently.  With ``scale``, the ulp is taken at magnitude
+    max(|want|, scale): for values computed as differences of terms of that size (a rotation), whose
+    inputs' last-bit differences do not shrink with the result."""
     g, w = got.float().cpu(), want.float().cpu()
     mant = {torch.bfloat16: 7, torch.float16: 10}[want.dtype]
-    ulp = torch.exp2(torch.floor(torch.log2(w.abs().clamp_min(1e-30))) - mant)
+    ulp = torch.exp2(torch.floor(torch.log2(w.abs().clamp_min(max(scale, 1e-30)))) - mant)
     bad = (g - w).abs() > ulps * ulp
     assert not bad.any(), (f"{what}: {int(bad.sum())} of {w.numel()} elements beyond {ulps} ulp; worst "
                            f"{((g - w).abs() / ulp).max().item():.1f} ulp")

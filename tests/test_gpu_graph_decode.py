@@ -111,11 +111,13 @@ def test_graph_decode_matches_eager_paged_decode(model_cfg, fused):
     assert cg.layers[0].store.seq_len() == T + steps
     # Layer 0's K/V depend only on the (teacher-forced) input tokens: the graph's paged writes went to
     # the same pages and slots as the eager writes, with the same bits (module path) or within the
-    # kernels' rounding of the norm and rotary arithmetic (fused path).
+    # rounding of the fused path (its q|k|v product sums K in another order; K then goes through the
+    # head RMSNorm and the rotation k1 cos - k2 sin, whose outputs near zero keep the last-bit
+    # differences of O(1) inputs, hence the ulp at magnitude 1 for K).
     ke, ve = ce.layers[0].store.gather()
     kg, vg = cg.layers[0].store.gather()
     if fused:
-        assert_within_ulps(kg, ke, 2, "layer-0 K pages")
+        assert_within_ulps(kg, ke, 2, "layer-0 K pages", scale=1.0)
         assert_within_ulps(vg, ve, 2, "layer-0 V pages")
     else:
         assert torch.equal(ke, kg) and torch.equal(ve, vg)

@@ -88,8 +88,10 @@ def test_swiglu_matches_silu_times_up():
     assert_within_ulps(out, want, 1, "swiglu")
 
 
+# The decode shapes of Qwen3-4B, M < 8 with ragged N, the largest K (10240), K not a multiple of 64.
 @pytest.mark.parametrize("M,N,K", [(8, 6144, 2560), (8, 2560, 4096), (8, 19456, 2560), (8, 2560, 9728),
-                                   (8, 151936, 2560), (3, 100, 2056), (1, 37, 8)])
+                                   (8, 151936, 2560), (5, 1000, 1024), (2, 300, 10240), (8, 2560, 4160),
+                                   (3, 100, 2056), (1, 37, 8)])
 def test_skinny_gemm_matches_fp32_product(M, N, K):
     _say(f"[layer-ops] gemm_skinny M={M} N={N} K={K}")
     x = _rand(M, K, seed=10 + M)
@@ -99,6 +101,20 @@ def test_skinny_gemm_matches_fp32_product(M, N, K):
     # one rounding of the output (half an ulp of bf16) plus fp32 summation in another order, which is
     # bounded by a small multiple of sum_k |x w| (it matters only where the sum nearly cancels)
     ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp_min(1e-30))) - 7)
+    bound = 0.5 * ulp + 1e-5 * (x.float().abs() @ w.float().abs().t())
+    bad = (out - want).abs() > bound
+    assert not bad.any(), f"{int(bad.sum())} of {out.numel()} outputs beyond the bound"
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 2560, 4096), (4, 77, 264)])
+def test_skinny_gemm_fp16(M, N, K):
+    """fp16 at a decode shape and at a small ragged one."""
+    _say(f"[layer-ops] gemm_skinny fp16 M={M} N={N} K={K}")
+    x = _rand(M, K, seed=30 + M).to(torch.float16)
+    w = (_rand(N, K, seed=40 + N % 97, scale=0.05)).to(torch.float16)
+    out = ops.gemm_skinny(x, w).float()
+    want = x.float() @ w.float().t()
+    ulp = torch.exp2(torch.floor(torch.log2(want.abs().clamp_min(1e-30))) - 10)
     bound = 0.5 * ulp + 1e-5 * (x.float().abs() @ w.float().abs().t())
     bad = (out - want).abs() > bound
     assert not bad.any(), f"{int(bad.sum())} of {out.numel()} outputs beyond the bound"
