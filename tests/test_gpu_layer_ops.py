@@ -88,10 +88,13 @@ def test_swiglu_matches_silu_times_up():
     assert_within_ulps(out, want, 1, "swiglu")
 
 
-# The decode shapes of Qwen3-4B, M < 8 with ragged N, the largest K (10240), K not a multiple of 64.
+# The decode shapes of Qwen3-4B (q|k|v, gate|up and the LM head on the LDS-staged matrix-core
+# kernel, o and down on the dot-product kernel), the matrix-core kernel with M < 8, ragged N and
+# one 128-wide K stage, then M < 8 with ragged N, the largest K (10240) and K not a multiple of 64
+# on the dot-product kernel.
 @pytest.mark.parametrize("M,N,K", [(8, 6144, 2560), (8, 2560, 4096), (8, 19456, 2560), (8, 2560, 9728),
-                                   (8, 151936, 2560), (5, 1000, 1024), (2, 300, 10240), (8, 2560, 4160),
-                                   (3, 100, 2056), (1, 37, 8)])
+                                   (8, 151936, 2560), (5, 6200, 1280), (1, 6150, 128), (5, 1000, 1024),
+                                   (2, 300, 10240), (8, 2560, 4160), (3, 100, 2056), (1, 37, 8)])
 def test_skinny_gemm_matches_fp32_product(M, N, K):
     _say(f"[layer-ops] gemm_skinny M={M} N={N} K={K}")
     x = _rand(M, K, seed=10 + M)
@@ -106,9 +109,9 @@ def test_skinny_gemm_matches_fp32_product(M, N, K):
     assert not bad.any(), f"{int(bad.sum())} of {out.numel()} outputs beyond the bound"
 
 
-@pytest.mark.parametrize("M,N,K", [(8, 2560, 4096), (4, 77, 264)])
+@pytest.mark.parametrize("M,N,K", [(8, 2560, 4096), (4, 77, 264), (8, 6144, 2560)])
 def test_skinny_gemm_fp16(M, N, K):
-    """fp16 at a decode shape and at a small ragged one."""
+    """fp16 on both kernels (N = 2560 and 6144) and at a small ragged shape."""
     _say(f"[layer-ops] gemm_skinny fp16 M={M} N={N} K={K}")
     x = _rand(M, K, seed=30 + M).to(torch.float16)
     w = (_rand(N, K, seed=40 + N % 97, scale=0.05)).to(torch.float16)
