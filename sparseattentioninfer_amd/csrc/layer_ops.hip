@@ -394,20 +394,16 @@ static void launch_skinny_r(const elem_t* x, int64_t x_st, const elem_t* w, int6
 }
 
 // ---- skinny GEMM on the matrix cores, W staged through LDS ----------------------------------
-// out[m, n] = sum_k x[m, k] * W[n, k] for M <= 8 and K a multiple of 128.  A workgroup of four
-// waves owns 64 output columns (16 per wave) over all of K, in stages of 128 K: the stage's W
-// rows (64 x 256 bytes) and x rows (8 x 256 bytes) go global -> LDS with direct loads in whole
+// out[m, n] = sum_k x[m, k] * W[n, k] for M <= 8 and K a multiple of 128.  A workgroup of NWV
+// waves owns 16 NWV output columns (16 per wave) over all of K, in stages of 128 K: the stage's W
+// rows (16 NWV x 256 bytes) and x rows (8 x 256 bytes) go global -> LDS with direct loads in whole
 // contiguous rows, each load permuting the 16-byte chunks of its row so that chunk c of row r
 // lands at position c ^ (r & 15).  Each wave then reads its 16 W rows (the B operand, one
 // k-chunk per 16-lane group: conflict-free thanks to the permutation) and the x rows (the A
 // operand; rows 8-15 of the 16-row product are never stored) and runs one v_mfma_f32_16x16x32
 // per 32 K.  SL_NS stages are in flight; one barrier per stage.
-constexpr int SL_TN = 64;
-constexpr int SL_KC = 128;
-constexpr int SL_NS = 4;
-constexpr int SL_WB = SL_TN * SL_KC * 2;  // W bytes per stage
-constexpr int SL_SB = SL_WB + 8 * SL_KC * 2;  // + x bytes
-constexpr int SL_LOADS = SL_WB / 1024 / 4 + 1;  // direct loads per wave per stage (4 W + 1 x)
+constexpr int SL_KC = 128;  // K per stage
+constexpr int SL_NS = 4;    // stages in flight
 
 __device__ __forceinline__ uint32_t sl_lds(const void* p) {
   return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)(p);
@@ -424,32 +420,45 @@ __device__ __forceinline__ void sl_load16(const void* vaddr, uint32_t lds) {
       : "memory", "m0");
 }
 
-template <bool BF16>
-__global__ __launch_bounds__(256) void skinny_lds_kernel(const elem_t* x, int64_t x_st, const elem_t* w,
-                                                         int64_t w_st, elem_t* out, int64_t out_st, int M, int N,
-                                                         int K) {
-  __shared__ __attribute__((aligned(16))) char sm[SL_NS * SL_SB];
+// NWV waves, 16 output columns each.  A stage holds the workgroup's 16 NWV W rows and the 8 x
+// rows (each wave loads its own W rows, 4 KiB, and 8 / NWV of the x rows).
+template <bool BF16, int NWV>
+__global__ __launch_bounds__(64 * NWV) void skinny_lds_kernel(const elem_t* x, int64_t x_st, const elem_t* w,
+                                                              int64_t w_st, elem_t* out, int64_t out_st, int M,
+                                                              int N, int K) {
+  constexpr int WB = 16 * NWV * SL_KC * 2;       // W bytes per stage
+  constexpr int SB = WB + 8 * SL_KC * 2;         // + x bytes
+  constexpr int XR = 8 / NWV;                    // x rows loaded per wave
+  constexpr int XI = (XR * 256 + 1023) / 1024;   // their direct loads
+  constexpr int LOADS = 4 + XI;                  // direct loads per wave per stage
+  __shared__ __attribute__((aligned(16))) char sm[SL_NS * SB];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int n0 = blockIdx.x * SL_TN;
+  const int n0 = blockIdx.x * 16 * NWV;
   const int nst = K / SL_KC;
   const int p = lane & 15;  // position within a 256-byte LDS row
-  // Load rows of this lane: W rows 16 wave + 4 i + lane / 16 (i < 4), x row 2 wave + lane / 16.
+  // This lane's load rows: W rows 16 wave + 4 i + lane / 16 (i < 4); x row XR wave + 4 j + lane / 16.
   const elem_t* wsrc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = 16 * wave + 4 * i + (lane >> 4);
     wsrc[i] = w + (int64_t)min(n0 + r, N - 1) * w_st + 8 * (p ^ (r & 15));
   }
-  const int xr = 2 * wave + (lane >> 4);
-  const elem_t* xsrc = x + (int64_t)min(xr, M - 1) * x_st + 8 * (p ^ (xr & 15));
+  const elem_t* xsrc[XI];
+#pragma unroll
+  for (int j = 0; j < XI; ++j) {
+    const int xr = XR * wave + 4 * j + (lane >> 4);
+    xsrc[j] = x + (int64_t)min(xr, M - 1) * x_st + 8 * (p ^ (xr & 15));
+  }
   const uint32_t base = sl_lds(sm);
   auto issue = [&](int st) {
-    const uint32_t b = base + (st % SL_NS) * SL_SB;
+    const uint32_t b = base + (st % SL_NS) * SB;
     const int k0 = st * SL_KC;
 #pragma unroll
     for (int i = 0; i < 4; ++i) sl_load16(wsrc[i] + k0, b + 1024 * (4 * wave + i));
-    if (lane < 32) sl_load16(xsrc + k0, b + SL_WB + 512 * wave);
+#pragma unroll
+    for (int j = 0; j < XI; ++j)
+      if (XR >= 4 || lane < XR * 16) sl_load16(xsrc[j] + k0, b + WB + 256 * XR * wave + 1024 * j);
   };
   // Operand offsets within a stage: B = W row 16 wave + lane % 16, A = x row (lane % 16) & 7;
   // k-chunk 4 ks + lane / 16.
@@ -462,19 +471,19 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(const elem_t* x, int64_
   for (int st = 0; st < nst; ++st) {
     const int after = min(SL_NS - 2, nst - 1 - st);  // stages issued after this one
     if (after >= 2)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * SL_LOADS & 15) | ((2 * SL_LOADS >> 4) << 14));
+      __builtin_amdgcn_s_waitcnt(0x0F70 | ((2 * LOADS) & 15) | (((2 * LOADS) >> 4) << 14));
     else if (after == 1)
-      __builtin_amdgcn_s_waitcnt(0x0F70 | SL_LOADS);
+      __builtin_amdgcn_s_waitcnt(0x0F70 | LOADS);
     else
       __builtin_amdgcn_s_waitcnt(0x0F70);
     __syncthreads();
     if (st + SL_NS - 1 < nst) issue(st + SL_NS - 1);
-    const char* sb = sm + (st % SL_NS) * SL_SB;
+    const char* sb = sm + (st % SL_NS) * SB;
 #pragma unroll
     for (int ks = 0; ks < SL_KC / 32; ++ks) {
       const int c = 4 * ks + g;
       const u32x4 bw = *reinterpret_cast<const u32x4*>(sb + rb * 256 + 16 * (c ^ (rb & 15)));
-      const u32x4 ax = *reinterpret_cast<const u32x4*>(sb + SL_WB + ra * 256 + 16 * (c ^ ra));
+      const u32x4 ax = *reinterpret_cast<const u32x4*>(sb + WB + ra * 256 + 16 * (c ^ ra));
       acc = Elem<BF16>::mfma16(ax, bw, acc);
     }
   }
@@ -487,6 +496,10 @@ __global__ __launch_bounds__(256) void skinny_lds_kernel(const elem_t* x, int64_
   }
 }
 
+// Two waves (32 columns) per workgroup: measured best against one and four at the Qwen3-4B decode
+// shapes with the weights streamed from HBM (q|k|v 8.0 us, gate|up 21 us, LM head 134 us).
+constexpr int SL_NWV = 2;
+
 // Dot-product kernel: rows per batch and workgroups per CU, measured at the Qwen3-4B decode shapes
 // with the weights streamed from HBM: wide products (N >= 64 per CU: gate|up, LM head) take 4 rows per batch and
 // three workgroups per CU; the others 2 rows, with four workgroups per CU while K fits two
@@ -495,11 +508,11 @@ template <bool BF16>
 static void launch_skinny(const elem_t* x, int64_t x_st, const elem_t* w, int64_t w_st, elem_t* out,
                           int64_t out_st, int M, int N, int K, hipStream_t s) {
   // Wide products with K a multiple of 128 run on the matrix cores with W staged through LDS
-  // (q|k|v, gate|up and the LM head of Qwen3-4B: 4-30 % faster); narrower ones (o, down: 40
+  // (q|k|v, gate|up and the LM head of Qwen3-4B: 20-30 % faster); narrower ones (o, down: 80
   // column tiles) keep more workgroups busy on the dot-product kernel.
   if (K % SL_KC == 0 && N >= 24 * num_cus_layer()) {
-    hipLaunchKernelGGL((skinny_lds_kernel<BF16>), dim3((N + SL_TN - 1) / SL_TN), dim3(256), 0, s, x, x_st, w, w_st,
-                       out, out_st, M, N, K);
+    hipLaunchKernelGGL((skinny_lds_kernel<BF16, SL_NWV>), dim3((N + 16 * SL_NWV - 1) / (16 * SL_NWV)),
+                       dim3(64 * SL_NWV), 0, s, x, x_st, w, w_st, out, out_st, M, N, K);
     return;
   }
   if (N >= 64 * num_cus_layer())
