@@ -240,6 +240,16 @@ int sa_swiglu(int dtype, const void* gate_up, int64_t gate_up_stride, void* out,
 int sa_gemm_skinny(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride, void* out,
                    int64_t out_stride, int M, int N, int K, void* stream);
 
+/*
+ * Qwen3MLP's gate and up projections and its SwiGLU for M <= 8 rows in one launch:
+ * w_gate_up holds the 2I gate and up rows interleaved (row 2i = gate row i, row 2i + 1 =
+ * up row i), and out[m, i] = round(round(silu(g)) * u) with g and u the bf16-rounded
+ * products of the pair -- the bits of sa_gemm_skinny on the concatenated [gate; up] rows
+ * followed by sa_swiglu.  K a multiple of 128.
+ */
+int sa_gemm_skinny_swiglu(int dtype, const void* x, int64_t x_stride, const void* w_gate_up, int64_t w_stride,
+                          void* out, int64_t out_stride, int M, int I, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,7 @@ SIGNATURES = {
     ]),
     "sa_swiglu": (_i32, [_i32, _vp, _i64, _vp, _i64, _i32, _i32, _vp]),
     "sa_gemm_skinny": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),
+    "sa_gemm_skinny_swiglu": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i32, _i32, _vp]),
 }
 
 

@@ -422,7 +422,10 @@ __device__ __forceinline__ void sl_load16(const void* vaddr, uint32_t lds) {
 
 // NWV waves, 16 output columns each.  A stage holds the workgroup's 16 NWV W rows and the 8 x
 // rows (each wave loads its own W rows, 4 KiB, and 8 / NWV of the x rows).
-template <bool BF16, int NWV>
+// ACT: W's rows are Qwen3MLP's gate and up rows interleaved (row 2i = gate i, row 2i + 1 = up i)
+// and out[m, i] = SwiGLU of the pair, rounded as sa_gemm_skinny then sa_swiglu round it (the
+// pair sits in adjacent lanes of one wave).
+template <bool BF16, int NWV, bool ACT>
 __global__ __launch_bounds__(64 * NWV) void skinny_lds_kernel(const elem_t* x, int64_t x_st, const elem_t* w,
                                                               int64_t w_st, elem_t* out, int64_t out_st, int M,
                                                               int N, int K) {
@@ -489,6 +492,19 @@ __global__ __launch_bounds__(64 * NWV) void skinny_lds_kernel(const elem_t* x, i
   }
   // D of the 16x16 product: lane l holds rows 4 (l / 16) + i of column l % 16.
   const int n = n0 + 16 * wave + p;
+  if constexpr (ACT) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = rnd<BF16>(acc[i]);     // the gate|up output as stored
+      const float u = __shfl_xor(v, 1, 64);  // up of the pair, for the even lane
+      const int m = 4 * g + i;
+      if (!(p & 1) && m < M && n + 1 < N) {
+        const float a = rnd<BF16>(v / (1.f + expf(-v)));
+        out[m * out_st + n / 2] = Elem<BF16>::from_f32(a * u);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = 4 * g + i;
@@ -511,7 +527,7 @@ static void launch_skinny(const elem_t* x, int64_t x_st, const elem_t* w, int64_
   // (q|k|v, gate|up and the LM head of Qwen3-4B: 20-30 % faster); narrower ones (o, down: 80
   // column tiles) keep more workgroups busy on the dot-product kernel.
   if (K % SL_KC == 0 && N >= 24 * num_cus_layer()) {
-    hipLaunchKernelGGL((skinny_lds_kernel<BF16, SL_NWV>), dim3((N + 16 * SL_NWV - 1) / (16 * SL_NWV)),
+    hipLaunchKernelGGL((skinny_lds_kernel<BF16, SL_NWV, false>), dim3((N + 16 * SL_NWV - 1) / (16 * SL_NWV)),
                        dim3(64 * SL_NWV), 0, s, x, x_st, w, w_st, out, out_st, M, N, K);
     return;
   }
@@ -547,4 +563,35 @@ extern "C" int sa_gemm_skinny(int dtype, const void* x, int64_t x_stride, const 
     launch_skinny<false>(xe, x_stride, we, w_stride, oe, out_stride, M, N, K, s);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? 0 : set_error((int)err, "sa_gemm_skinny: launch failed: %s", hipGetErrorString(err));
+}
+
+extern "C" int sa_gemm_skinny_swiglu(int dtype, const void* x, int64_t x_stride, const void* w_gate_up,
+                                     int64_t w_stride, void* out, int64_t out_stride, int M, int I, int K,
+                                     void* stream) {
+  using namespace sa;
+  clear_error();
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F16)
+    return set_error(SA_E_DTYPE, "sa_gemm_skinny_swiglu: dtype %d is not bf16 (0) or f16 (1)", dtype);
+  if (M < 0 || M > SK_M || I < 0 || K < SL_KC || K % SL_KC)
+    return set_error(SA_E_SHAPE, "sa_gemm_skinny_swiglu: M=%d (<= %d), I=%d, K=%d (a multiple of %d)", M, SK_M, I,
+                     K, SL_KC);
+  if (M == 0 || I == 0) return 0;
+  if (!x || !w_gate_up || !out) return set_error(SA_E_NULL, "sa_gemm_skinny_swiglu: NULL pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_gate_up)) & 15 || x_stride % 8 || w_stride % 8)
+    return set_error(SA_E_ALIGN, "sa_gemm_skinny_swiglu: x and W rows must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int N = 2 * I;
+  const dim3 g((N + 16 * SL_NWV - 1) / (16 * SL_NWV)), b(64 * SL_NWV);
+  auto xe = static_cast<const elem_t*>(x);
+  auto we = static_cast<const elem_t*>(w_gate_up);
+  auto oe = static_cast<elem_t*>(out);
+  if (dtype == SA_DTYPE_BF16)
+    hipLaunchKernelGGL((skinny_lds_kernel<true, SL_NWV, true>), g, b, 0, s, xe, x_stride, we, w_stride, oe,
+                       out_stride, M, N, K);
+  else
+    hipLaunchKernelGGL((skinny_lds_kernel<false, SL_NWV, true>), g, b, 0, s, xe, x_stride, we, w_stride, oe,
+                       out_stride, M, N, K);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0
+                           : set_error((int)err, "sa_gemm_skinny_swiglu: launch failed: %s", hipGetErrorString(err));
 }

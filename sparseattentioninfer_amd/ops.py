@@ -486,3 +486,31 @@ def gemm_skinny(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = Non
                                         out.data_ptr(), out.stride(0), M, N, K, _stream(x))
     _lib.check("sa_gemm_skinny", status)
     return out
+
+
+def interleave_gate_up(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``[I, K]`` gate and up weights as one ``[2I, K]`` tensor with row 2i = gate row i and row
+    2i + 1 = up row i (the layout ``gemm_skinny_swiglu`` reads)."""
+    _require(gate.shape == up.shape and gate.dim() == 2 and gate.dtype == up.dtype, "interleave_gate_up: shapes")
+    return torch.stack([gate, up], dim=1).reshape(2 * gate.size(0), gate.size(1)).contiguous()
+
+
+def gemm_skinny_swiglu(x: torch.Tensor, w_gate_up: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """SwiGLU of the gate and up projections of ``x [M, K]`` (M <= 8) in one launch, from the
+    interleaved weights of :func:`interleave_gate_up`: the bits of ``gemm_skinny`` on the
+    concatenated ``[gate; up]`` rows followed by ``swiglu``."""
+    name = "gemm_skinny_swiglu"
+    _require(x.is_cuda and w_gate_up.is_cuda and x.dim() == 2 and w_gate_up.dim() == 2 and x.dtype in _DTYPES
+             and w_gate_up.dtype == x.dtype and x.stride(1) == 1 and w_gate_up.stride(1) == 1, f"{name}: bad operands")
+    M, K = x.shape
+    N2 = w_gate_up.size(0)
+    _require(w_gate_up.size(1) == K and M <= 8 and N2 % 2 == 0 and K % 128 == 0,
+             f"{name}: M={M} (<= 8), K={K} (a multiple of 128), {N2} weight rows (even)")
+    I = N2 // 2
+    if out is None:
+        out = torch.empty(M, I, dtype=x.dtype, device=x.device)
+    _require(out.shape == (M, I) and out.stride(1) == 1 and out.dtype == x.dtype, f"{name}: bad out")
+    status = _lib.load().sa_gemm_skinny_swiglu(_DTYPES[x.dtype], x.data_ptr(), x.stride(0), w_gate_up.data_ptr(),
+                                               w_gate_up.stride(0), out.data_ptr(), out.stride(0), M, I, K, _stream(x))
+    _lib.check("sa_gemm_skinny_swiglu", status)
+    return out

@@ -19,13 +19,14 @@ the decoder builds it for every ``qb`` the run can reach with the layer's own
 pattern (``pattern.build`` and the backend's schedule, exactly as the eager
 path does per step) and gathers row ``qb`` on the device.
 
-With ``fused=True`` (the default) a layer is nine launches: one GEMM for the
+With ``fused=True`` (the default) a layer is eight launches: one GEMM for the
 concatenated q|k|v projection (``sa_gemm_skinny``, which streams the weights
 once for the batch's few rows), ``sa_qk_rope_kv`` (q/k RMSNorm, rotary
 embedding, paged K/V write), the paged decode kernel, the output GEMM,
-``sa_rmsnorm`` (residual add + post-attention norm), one GEMM for the
-concatenated gate|up projection, ``sa_swiglu``, the down GEMM and ``sa_rmsnorm``
-(residual add + the next layer's input norm).  ``fused=False`` calls the model's
+``sa_rmsnorm`` (residual add + post-attention norm), one GEMM for the gate and
+up projections with the SwiGLU in its epilogue (``sa_gemm_skinny_swiglu``, on
+the weights interleaved once), the down GEMM and ``sa_rmsnorm`` (residual add +
+the next layer's input norm).  ``fused=False`` calls the model's
 own modules instead (Hugging Face's arithmetic op by op, about 66 launches per
 layer).
 
@@ -187,7 +188,7 @@ class GraphDecoder:
         for layer in self.layers:
             a, mlp = layer.self_attn, layer.mlp
             self.w_qkv.append(torch.cat([a.q_proj.weight, a.k_proj.weight, a.v_proj.weight], 0).contiguous())
-            self.w_gu.append(torch.cat([mlp.gate_proj.weight, mlp.up_proj.weight], 0).contiguous())
+            self.w_gu.append(ops.interleave_gate_up(mlp.gate_proj.weight, mlp.up_proj.weight))
         hidden = cfg.hidden_size
         H, D = self.num_heads, self.head_dim
         new = lambda *shape: torch.empty(*shape, dtype=dt, device=dev)  # noqa: E731
@@ -197,7 +198,6 @@ class GraphDecoder:
         self.qkv = new(B, self.w_qkv[0].size(0))
         self.q = new(B, H, D)
         self.att = new(B, H, D)
-        self.gu = new(B, self.w_gu[0].size(0))
         self.mid = new(B, self.w_gu[0].size(0) // 2)
         inter = self.mid.size(1)
         self.down_skinny = inter % 8 == 0 and inter <= 10240  # sa_gemm_skinny's K limit
@@ -229,8 +229,7 @@ class GraphDecoder:
                 out=self.att)
             ops.gemm_skinny(self.att.view(B, -1), attn.o_proj.weight, out=self.a)
             ops.rmsnorm(self.a, layer.post_attention_layernorm.weight, self.eps, residual=self.h, out=self.x)
-            ops.gemm_skinny(self.x, self.w_gu[i], out=self.gu)
-            ops.swiglu(self.gu, out=self.mid)
+            ops.gemm_skinny_swiglu(self.x, self.w_gu[i], out=self.mid)
             if self.down_skinny:
                 ops.gemm_skinny(self.mid, layer.mlp.down_proj.weight, out=self.a)
             else:

@@ -121,3 +121,17 @@ def test_skinny_gemm_fp16(M, N, K):
     bound = 0.5 * ulp + 1e-5 * (x.float().abs() @ w.float().abs().t())
     bad = (out - want).abs() > bound
     assert not bad.any(), f"{int(bad.sum())} of {out.numel()} outputs beyond the bound"
+
+
+@pytest.mark.parametrize("M,I,K", [(8, 9728, 2560), (5, 3100, 1280), (1, 3072, 128)])
+def test_gemm_skinny_swiglu(M, I, K):
+    """Gate|up product with the SwiGLU in its epilogue, on interleaved weights, gives the bits of the
+    product on the concatenated weights followed by sa_swiglu (both products on the matrix-core
+    kernel: 2I >= 6144 columns); with a ragged last column tile and a single 128-wide K stage."""
+    _say(f"[layer-ops] gemm_skinny_swiglu M={M} I={I} K={K}")
+    x = _rand(M, K, seed=130 + M)
+    gate = _rand(I, K, seed=140 + I % 97, scale=0.05)
+    up = _rand(I, K, seed=150 + I % 97, scale=0.05)
+    fused = ops.gemm_skinny_swiglu(x, ops.interleave_gate_up(gate, up))
+    two = ops.swiglu(ops.gemm_skinny(x, torch.cat([gate, up], 0).contiguous()))
+    assert torch.equal(fused, two)
