@@ -90,17 +90,11 @@ class _LayerSchedule:
         for i, r in enumerate(rows):
             self.table[i, :, :r.size(1)] = r
         self.counts = torch.stack(counts).to(device)              # [n_qb, R]
-        self.sel = torch.zeros(1, R, self.width, dtype=torch.int32, device=device)
-        self.sel_off = torch.zeros(1, R, 2, dtype=torch.int32, device=device)
+        self.sel = self.sel_off = None  # views of the decoder's gathered selections (set by the decoder)
         self.rows = R
         self.num_splits = ops.auto_decode_splits(batch, R, self.width)
         need = ops.decode_workspace_bytes(batch, H, D, self.num_splits)
         self.workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
-
-    def select(self, qb_rel: torch.Tensor) -> None:
-        """Copies the selection of query block ``qb0 + qb_rel`` (a device index) into the buffers."""
-        self.sel.copy_(self.table.index_select(0, qb_rel))
-        self.sel_off[:, :, 1].copy_(self.counts.index_select(0, qb_rel))
 
 
 class GraphDecoder:
@@ -153,6 +147,7 @@ class GraphDecoder:
                 sched[key] = _LayerSchedule(attn, store, qb0, qb1, self.B, self.dev)
             self.sched.append(sched[key])
         self.uniq_sched = list(sched.values())
+        self._merge_selections()
         # device state
         self.ids = ids.reshape(self.B).to(torch.long).clone()
         self.pos = torch.full((1,), self.start, dtype=torch.long, device=self.dev)
@@ -212,8 +207,7 @@ class GraphDecoder:
         ops.rmsnorm(self.h, self.layers[0].input_layernorm.weight, self.eps, out=self.x)
         qb_rel = torch.div(self.pos, self.page, rounding_mode="floor") - self.qb0
         self.kv_lens.copy_((self.pos + 1).to(torch.int32).expand(self.B))
-        for s in self.uniq_sched:
-            s.select(qb_rel)
+        self._select(qb_rel)
         B = self.B
         # Every projection on the skinny GEMM (the down projection on hipBLASLt when its K, the
         # intermediate size, is past the skinny kernel's limit).
@@ -242,6 +236,30 @@ class GraphDecoder:
         self.ids.copy_(_argmax_rows(self.lg, self.chunk))
         self.pos.add_(1)
 
+    def _merge_selections(self) -> None:
+        """Stacks every schedule's selection table into one, so that a step gathers the selections of
+        all layers with two launches; each schedule's ``sel`` / ``sel_off`` become views of the
+        gathered buffers (the decode kernel takes their row strides)."""
+        S = len(self.uniq_sched)
+        R = max(s.rows for s in self.uniq_sched)
+        W = max(s.width for s in self.uniq_sched)
+        nqb = self.uniq_sched[0].table.size(0)
+        self.sel_table = torch.zeros(nqb, S, R, W, dtype=torch.int32, device=self.dev)
+        self.off_table = torch.zeros(nqb, S, R, 2, dtype=torch.int32, device=self.dev)
+        for i, s in enumerate(self.uniq_sched):
+            self.sel_table[:, i, :s.rows, :s.width] = s.table
+            self.off_table[:, i, :s.rows, 1] = s.counts
+        self.sel_all = torch.zeros(1, S, R, W, dtype=torch.int32, device=self.dev)
+        self.off_all = torch.zeros(1, S, R, 2, dtype=torch.int32, device=self.dev)
+        for i, s in enumerate(self.uniq_sched):
+            s.sel = self.sel_all[:, i, :s.rows, :s.width]
+            s.sel_off = self.off_all[:, i, :s.rows, :]
+
+    def _select(self, qb_rel: torch.Tensor) -> None:
+        """Gathers the selections of query block ``qb0 + qb_rel`` (a device index) for every layer."""
+        torch.index_select(self.sel_table, 0, qb_rel, out=self.sel_all)
+        torch.index_select(self.off_table, 0, qb_rel, out=self.off_all)
+
     def _step(self) -> None:
         if self.fused:
             self._step_fused()
@@ -257,8 +275,7 @@ class GraphDecoder:
         qb_rel = torch.div(self.pos, page, rounding_mode="floor") - self.qb0    # [1]
         slot = (self.pos % page).expand(B)                                      # [B]
         kv_len = (self.pos + 1).to(torch.int32).expand(B)
-        for s in self.uniq_sched:
-            s.select(qb_rel)
+        self._select(qb_rel)
         for layer, store, sched in zip(self.layers, self.stores, self.sched):
             attn = layer.self_attn
             res = h
