@@ -199,7 +199,8 @@ int64_t sa_decode_workspace_bytes(int B, int Hq, int D, int num_splits);
  * (transformers/models/qwen3/modeling_qwen3.py, Qwen3DecoderLayer.forward):
  * for each of `rows` rows of n elements, r = residual + x rounded and stored
  * back into residual when residual is not NULL (else r = x), then
- * out = weight * round(r * rsqrt(mean(r^2) + eps)), rounded.  n <= 8192.
+ * out = weight * round(r * rsqrt(mean(r^2) + eps)), rounded.  n a multiple of 8
+ * and at most 8192; rows 16-byte aligned.
  */
 int sa_rmsnorm(int dtype, const void* x, int64_t x_stride, void* residual, int64_t residual_stride,
                const void* weight, void* out, int64_t out_stride, int rows, int n, float eps, void* stream);

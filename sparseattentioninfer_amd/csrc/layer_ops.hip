@@ -31,11 +31,19 @@ __device__ __forceinline__ float wave_sum(float x) {
   return x;
 }
 
-constexpr int NORM_THREADS = 1024;
-constexpr int NORM_MAX_PER_THREAD = 8;  // hidden sizes up to 8192
+constexpr int NORM_THREADS = 256;
+constexpr int NORM_MAX_CHUNKS = 4;  // 16-byte chunks (8 elements) per thread: hidden sizes up to 8192
+
+template <bool BF16>
+__device__ __forceinline__ float lo_f(uint32_t v) { return Elem<BF16>::to_f32((elem_t)(v & 0xffffu)); }
+template <bool BF16>
+__device__ __forceinline__ float hi_f(uint32_t v) { return Elem<BF16>::to_f32((elem_t)(v >> 16)); }
 
 // One workgroup per row: r = residual + x (rounded; stored back) when residual is given,
-// else r = x; out = w * rnd(r * rsqrt(mean(r^2) + eps)) rounded.
+// else r = x; out = w * rnd(r * rsqrt(mean(r^2) + eps)) rounded.  n a multiple of 8 and rows
+// 16-byte aligned: thread t owns the 16-byte chunks t, t + NORM_THREADS, ...  Every load of the
+// row is issued before the first store: the stores may alias the inputs as far as the compiler
+// knows, so interleaving them would serialise the row into one memory round trip per chunk.
 template <bool BF16>
 __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(const elem_t* x, int64_t x_st, elem_t* res,
                                                                int64_t res_st, const elem_t* w, elem_t* out,
@@ -43,38 +51,41 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(const elem_t* x, 
   __shared__ float s_part[NORM_THREADS / 64];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
+  const int nch = n / 8;
   const elem_t* xr = x + row * x_st;
   elem_t* rr = res ? res + row * res_st : nullptr;
-  // Every load of the row (x, residual, weight) is issued before the first store: the stores
-  // may alias the inputs as far as the compiler knows, so interleaving them would serialise
-  // the row into one memory round trip per element slot.
-  float xv[NORM_MAX_PER_THREAD], rv[NORM_MAX_PER_THREAD], wv[NORM_MAX_PER_THREAD];
+  u32x4 xv[NORM_MAX_CHUNKS], rv[NORM_MAX_CHUNKS], wv[NORM_MAX_CHUNKS];
 #pragma unroll
-  for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
-    const int i = tid + u * NORM_THREADS;
-    xv[u] = rv[u] = wv[u] = 0.f;
-    if (i < n) {
-      xv[u] = ld<BF16>(xr + i);
-      if (rr) rv[u] = ld<BF16>(rr + i);
-      wv[u] = ld<BF16>(w + i);
+  for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
+    const int c = tid + j * NORM_THREADS;
+    xv[j] = rv[j] = wv[j] = u32x4{0u, 0u, 0u, 0u};
+    if (c < nch) {
+      xv[j] = *reinterpret_cast<const u32x4*>(xr + 8 * c);
+      if (rr) rv[j] = *reinterpret_cast<const u32x4*>(rr + 8 * c);
+      wv[j] = *reinterpret_cast<const u32x4*>(w + 8 * c);
     }
   }
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
-    const int i = tid + u * NORM_THREADS;
-    if (i < n) {
-      float r = xv[u];
-      if (rr) r = rnd<BF16>(rv[u] + r);
-      xv[u] = r;
-      ss += r * r;
+  for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
+    if (tid + j * NORM_THREADS >= nch) continue;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float l = lo_f<BF16>(xv[j][e]), h = hi_f<BF16>(xv[j][e]);
+      if (rr) {
+        l = rnd<BF16>(lo_f<BF16>(rv[j][e]) + l);
+        h = rnd<BF16>(hi_f<BF16>(rv[j][e]) + h);
+      }
+      ss += l * l;
+      ss += h * h;
+      xv[j][e] = Elem<BF16>::pack2f(l, h);
     }
   }
   if (rr) {
 #pragma unroll
-    for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
-      const int i = tid + u * NORM_THREADS;
-      if (i < n) rr[i] = Elem<BF16>::from_f32(xv[u]);
+    for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
+      const int c = tid + j * NORM_THREADS;
+      if (c < nch) *reinterpret_cast<u32x4*>(rr + 8 * c) = xv[j];
     }
   }
   ss = wave_sum(ss);
@@ -86,9 +97,15 @@ __global__ __launch_bounds__(NORM_THREADS) void rmsnorm_kernel(const elem_t* x, 
   const float inv = rsqrtf(tot / (float)n + eps);
   elem_t* orow = out + row * out_st;
 #pragma unroll
-  for (int u = 0; u < NORM_MAX_PER_THREAD; ++u) {
-    const int i = tid + u * NORM_THREADS;
-    if (i < n) orow[i] = Elem<BF16>::from_f32(wv[u] * rnd<BF16>(xv[u] * inv));
+  for (int j = 0; j < NORM_MAX_CHUNKS; ++j) {
+    const int c = tid + j * NORM_THREADS;
+    if (c >= nch) continue;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      o[e] = Elem<BF16>::pack2f(lo_f<BF16>(wv[j][e]) * rnd<BF16>(lo_f<BF16>(xv[j][e]) * inv),
+                                hi_f<BF16>(wv[j][e]) * rnd<BF16>(hi_f<BF16>(xv[j][e]) * inv));
+    *reinterpret_cast<u32x4*>(orow + 8 * c) = o;
   }
 }
 
@@ -167,11 +184,14 @@ extern "C" int sa_rmsnorm(int dtype, const void* x, int64_t x_stride, void* resi
   clear_error();
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F16)
     return set_error(SA_E_DTYPE, "sa_rmsnorm: dtype %d is not bf16 (0) or f16 (1)", dtype);
-  if (rows < 0 || n < 1 || n > NORM_THREADS * NORM_MAX_PER_THREAD)
-    return set_error(SA_E_SHAPE, "sa_rmsnorm: rows=%d, n=%d (1 <= n <= %d)", rows, n,
-                     NORM_THREADS * NORM_MAX_PER_THREAD);
+  if (rows < 0 || n < 8 || n % 8 || n > NORM_THREADS * NORM_MAX_CHUNKS * 8)
+    return set_error(SA_E_SHAPE, "sa_rmsnorm: rows=%d, n=%d (a multiple of 8, 8 <= n <= %d)", rows, n,
+                     NORM_THREADS * NORM_MAX_CHUNKS * 8);
   if (rows == 0) return 0;
   if (!x || !weight || !out) return set_error(SA_E_NULL, "sa_rmsnorm: NULL tensor pointer");
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(weight) |
+       reinterpret_cast<uintptr_t>(out)) & 15 || x_stride % 8 || out_stride % 8 || (residual && residual_stride % 8))
+    return set_error(SA_E_ALIGN, "sa_rmsnorm: rows must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(stream);
   auto xe = static_cast<const elem_t*>(x);
   auto re = static_cast<elem_t*>(residual);

@@ -409,6 +409,7 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, *, residual: torc
     name = "rmsnorm"
     _require(x.is_cuda and x.dim() == 2 and x.stride(1) == 1 and x.dtype in _DTYPES, f"{name}: bad x")
     rows, n = x.shape
+    _require(n % 8 == 0 and n <= 8192, f"{name}: n={n} (a multiple of 8, at most 8192)")
     _require(weight.shape == (n,) and weight.dtype == x.dtype and weight.is_contiguous(), f"{name}: bad weight")
     if residual is not None:
         _require(residual.shape == x.shape and residual.dtype == x.dtype and residual.stride(1) == 1,
