@@ -109,6 +109,10 @@ CASES = [
     ("b16_chunk_tail", 1, 4, 2, 200, 1010, 128, 16, "bernoulli0.3", "kv", torch.bfloat16),
     ("b32_fp16_group", 1, 8, 2, 640, 640, 128, 32, "bernoulli0.2", "kv", torch.float16),
     ("b16_cfg2_slice", 1, 32, 8, 2048, 2048, 128, 16, "bernoulli0.05", "kv", torch.bfloat16),
+    # four-head kernel over rows of about 94 tiles (the schedule is read 64 positions at a time) and
+    # of 625 tiles (past the 512-entry LDS cache of the sub-block kernels: read from global memory)
+    ("b16_long_rows", 1, 8, 2, 256, 6000, 128, 16, "bernoulli0.5", "kv", torch.bfloat16),
+    ("b32_uncached_rows", 1, 4, 1, 64, 40000, 128, 32, "bernoulli0.6", "kv", torch.bfloat16),
 ]
 
 
