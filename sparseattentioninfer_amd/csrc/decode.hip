@@ -320,6 +320,10 @@ __global__ __launch_bounds__(64 * DEC_WAVES) __attribute__((amdgpu_waves_per_eu(
 }
 
 // Merges split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
+// The partials are read COMB_CHUNK splits at a time, every load of a chunk issued before the first
+// is used (one memory round trip per chunk, not one per split); chunks merge online. With at most
+// COMB_CHUNK splits, M and the summation order are those of a plain loop over s.
+constexpr int COMB_CHUNK = 16;
 template <bool BF16>
 __global__ void decode_combine_kernel(const float* part, elem_t* o, int64_t o_sb, int64_t o_sh,
                                       int B, int Hq, int D, int S) {
@@ -328,16 +332,33 @@ __global__ void decode_combine_kernel(const float* part, elem_t* o, int64_t o_sb
   const int b = bh / Hq, h = bh % Hq;
   const int64_t stride_s = (int64_t)B * Hq * (D + 2);
   const float* p0 = part + (int64_t)bh * (D + 2);
-  float M = -__builtin_inff();
-  for (int s = 0; s < S; ++s) M = fmaxf(M, p0[s * stride_s + D]);
-  const float Mu = M == -__builtin_inff() ? 0.f : M;
   for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float Ls = 0.f, As = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const float* ps = p0 + s * stride_s;
-      const float f = fast_exp2(ps[D] - Mu);
-      Ls += ps[D + 1] * f;
-      As += ps[d] * f;
+    float M = -__builtin_inff(), Ls = 0.f, As = 0.f;
+    for (int s0 = 0; s0 < S; s0 += COMB_CHUNK) {
+      float m[COMB_CHUNK], l[COMB_CHUNK], v[COMB_CHUNK];
+#pragma unroll
+      for (int i = 0; i < COMB_CHUNK; ++i) {
+        const float* ps = p0 + min(s0 + i, S - 1) * stride_s;  // past S: a repeat, skipped below
+        m[i] = ps[D];
+        l[i] = ps[D + 1];
+        v[i] = ps[d];
+      }
+      float Mc = M;
+#pragma unroll
+      for (int i = 0; i < COMB_CHUNK; ++i)
+        if (s0 + i < S) Mc = fmaxf(Mc, m[i]);
+      const float Mu = Mc == -__builtin_inff() ? 0.f : Mc;
+      const float r = fast_exp2(M - Mu);  // 0 while nothing has been merged (M = -inf)
+      Ls *= r;
+      As *= r;
+#pragma unroll
+      for (int i = 0; i < COMB_CHUNK; ++i)
+        if (s0 + i < S) {
+          const float f = fast_exp2(m[i] - Mu);
+          Ls += l[i] * f;
+          As += v[i] * f;
+        }
+      M = Mc;
     }
     o[b * o_sb + h * o_sh + d] = E::from_f32(Ls > 0.f ? As / Ls : 0.f);
   }

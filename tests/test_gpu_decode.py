@@ -46,6 +46,10 @@ DCASES = [
     ("page16_d64", 3, 4, 4, 64, 16, [17, 300, 1000], "kv", 1, torch.bfloat16),
     ("page128", 2, 8, 2, 128, 128, [1000, 129], "kv", 2, torch.bfloat16),
     ("fp16", 2, 8, 2, 128, 64, [999, 3000], "kv", 1, torch.float16),
+    # the combine reads 16 splits per memory round trip: exactly one chunk, then a second chunk with
+    # more splits than retained blocks (empty splits carry m = -inf, l = 0)
+    ("splits16", 2, 8, 2, 128, 64, [9000, 2100], "kv", 16, torch.bfloat16),
+    ("splits21_empty", 3, 8, 2, 128, 64, [5000, 700, 64], "kv", 21, torch.bfloat16),
 ]
 
 
