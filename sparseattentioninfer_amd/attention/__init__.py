@@ -29,9 +29,19 @@ def register_backend(name: str, cls: type[AttentionBackend]) -> None:
     _REGISTRY[name] = cls
 
 
-def register_into(registry: dict) -> None:
-    """Adds this backend to another registry dict (e.g. the reference's ``_REGISTRY``)."""
-    registry[BACKEND_NAME] = HipBlockSparseBackend
+def register_into(registry: dict, fallback=None) -> type[AttentionBackend]:
+    """Adds this backend to another registry dict (e.g. the reference's ``_REGISTRY``).
+
+    ``fallback`` (a backend class or instance, e.g. the reference's ``MaskedSdpaBackend``)
+    restores the reference backends' contract (``triton_universal_backend.py:47-66``): inputs
+    the kernels cannot take run there and ``actual_backend`` reads ``"masked_sdpa_fallback"``.
+    Without it such inputs raise.  Returns the registered class.
+    """
+    cls = HipBlockSparseBackend
+    if fallback is not None:
+        cls = type("HipBlockSparseBackendWithFallback", (HipBlockSparseBackend,), {"default_fallback": fallback})
+    registry[BACKEND_NAME] = cls
+    return cls
 
 
 __all__ = ["AttentionBackend", "HipBlockSparseBackend", "get_backend", "register_backend", "register_into",

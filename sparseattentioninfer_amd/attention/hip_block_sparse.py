@@ -9,9 +9,17 @@ padded ``kv_block_list``, plus ``block_size``).
 
 Differences from the reference, all deliberate:
 
-* No silent fallback.  Where the Triton backends quietly run the dense masked
-  path (CPU tensors, fp32, no block schedule), this backend raises, so a run
-  either executes the HIP kernels or fails loudly.
+* Fallback only when the caller supplies one.  The reference's Triton backends
+  run ``MaskedSdpaBackend`` for inputs their kernel cannot take (CPU tensors,
+  dtypes other than fp16/bf16, no block schedule or block size) and report
+  ``actual_backend == "masked_sdpa_fallback"``
+  (``triton_universal_backend.py:47-66``).  This backend does the same for
+  exactly those inputs (and top-k patterns) when it is constructed with
+  ``fallback=`` -- inside the reference, its own ``MaskedSdpaBackend`` class,
+  injected by :func:`~sparseattentioninfer_amd.attention.register_into`.
+  Without one it raises.  A missing or broken HIP library is never a reason to
+  fall back: GPU fp16/bf16 inputs with a schedule always run the kernels or
+  raise.
 * ``k``/``v`` may carry ``H_kv < H`` heads (grouped-query attention); the
   caller need not ``repeat_kv``.  A CSR with ``H_kv`` rows is shared by the
   query heads of each KV group, letting one K/V tile feed all of them.
@@ -65,8 +73,14 @@ class HipBlockSparseBackend(AttentionBackend):
     """Block-sparse attention on hand-written HIP kernels for gfx950."""
 
     supports_gqa = True   # k/v may carry H_kv < H heads; callers need not repeat them
+    FALLBACK_NAME = "masked_sdpa_fallback"
+    # Backend class or instance used for inputs the kernels cannot take; subclasses made by
+    # register_into(..., fallback=cls) set it, so the registry's no-argument construction has it.
+    default_fallback = None
 
-    def __init__(self):
+    def __init__(self, fallback=None):
+        fb = fallback if fallback is not None else self.default_fallback
+        self._fallback = fb() if isinstance(fb, type) else fb
         self._last_actual_backend = "unknown"
         self.last_kernel = None          # "prefill" or "decode" after a forward
         self._dense_cache: dict = {}
@@ -125,11 +139,45 @@ class HipBlockSparseBackend(AttentionBackend):
             f"hip_block_sparse does not run pattern kind {pattern.kind!r} (data-dependent top-k "
             "selection is not a block schedule)")
 
+    @staticmethod
+    def unsupported_reason(q: torch.Tensor, pattern: PatternMetadata):
+        """Why the kernels cannot take these inputs (the reference backends' fallback conditions,
+        ``triton_universal_backend.py:54-61``, plus top-k patterns), or None when they can."""
+        if not q.is_cuda:
+            return "a CPU tensor"
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            return f"dtype {q.dtype} (the kernels take float16 and bfloat16)"
+        if pattern.kind in ("mask", "local"):
+            if pattern.block_size is None:
+                return "pattern.block_size is None"
+            if (pattern.block_pairs is None or pattern.block_pair_offsets is None) and pattern.kv_block_list is None:
+                return "no block schedule (block_pairs/block_pair_offsets or kv_block_list)"
+        elif pattern.kind != "dense":
+            return f"pattern kind {pattern.kind!r} (data-dependent top-k selection is not a block schedule)"
+        return None
+
+    def _run_fallback(self, q, k, v, pattern, reason: str) -> torch.Tensor:
+        if self._fallback is None:
+            if not q.is_cuda:
+                raise RuntimeError("hip_block_sparse runs on ROCm GPU tensors only; got a CPU tensor "
+                                   "(no fallback backend was given)")
+            if pattern.kind not in ("mask", "local", "dense"):
+                raise NotImplementedError(f"hip_block_sparse does not run {reason}; no fallback backend was given")
+            raise ValueError(f"hip_block_sparse cannot run {reason}; no fallback backend was given")
+        # The reference's backends take K/V with the query's head count (its callers repeat them).
+        n_rep = q.size(1) // k.size(1)
+        if n_rep > 1:
+            k = k[:, :, None].expand(-1, -1, n_rep, -1, -1).reshape(q.size(0), q.size(1), k.size(2), k.size(3))
+            v = v[:, :, None].expand(-1, -1, n_rep, -1, -1).reshape(q.size(0), q.size(1), v.size(2), v.size(3))
+        self._last_actual_backend = self.FALLBACK_NAME
+        self.last_kernel = None
+        return self._fallback.forward(q, k, v, pattern)
+
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                 pattern: PatternMetadata) -> torch.Tensor:
-        if not q.is_cuda:
-            raise RuntimeError("hip_block_sparse runs on ROCm GPU tensors only; got a CPU tensor "
-                               "(this backend has no CPU fallback)")
+        reason = self.unsupported_reason(q, pattern)
+        if reason is not None:
+            return self._run_fallback(q, k, v, pattern, reason)
         pairs, offsets, bs = self._schedule(q.size(2), k.size(2), k.size(1), q.device, pattern)
         tiles = self._tiles(pairs, offsets, bs) if q.size(2) > 1 else None
         out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs, tiles=tiles)

@@ -35,15 +35,13 @@ from ..models.attention_layer import repeat_kv
 from ..patterns import (BigBirdKeepRatioPattern, BigBirdPattern, DenseCausalPattern, LocalWindowPattern,
                         SeededBigBirdPattern)
 from .paged_cache import PagedKVCache
-from .sparse_config import (_compute_pattern_stats, _ensure_attn_implementation, _get_config_attr,
-                            _is_plain_causal_mask, _materialize_layer_group_sparsities,
-                            _normalize_group_sparsities, _normalize_layer_group_sparsities,
-                            _resolve_backend_candidates, validate_sparse_kernel_runtime)
+from .sparse_config import (GroupSparsitySpec, backend_candidates, config_value, ensure_attn_implementation,
+                            is_plain_causal_mask, pattern_stats, validate_sparse_kernel_runtime)
 
 
 def _layer_pattern_name(config, layer_idx: int) -> str:
-    name = _get_config_attr(config, "sparse_attention_pattern", "local")
-    layers = _get_config_attr(config, "sparse_attention_layers", None)
+    name = config_value(config, "sparse_attention_pattern", "local")
+    layers = config_value(config, "sparse_attention_layers", None)
     if layers is not None and layer_idx not in set(int(i) for i in layers):
         return "dense"
     return name
@@ -58,22 +56,15 @@ class Qwen3SparseKernelAttention(Qwen3Attention):
         self.num_heads = config.num_attention_heads
         self.num_key_value_heads = config.num_key_value_heads
         pattern_name = _layer_pattern_name(config, layer_idx)
-        raw_backend = backend_name or _get_config_attr(config, "sparse_attention_backend", "auto")
-        window_size = window_size or _get_config_attr(config, "sparse_attention_window_size", 512)
-        block_size = block_size or _get_config_attr(config, "sparse_attention_block_size", 64)
-        top_k = _get_config_attr(config, "sparse_attention_top_k", 128)
-        keep_ratio = _get_config_attr(config, "sparse_attention_keep_ratio", None)
-        groups = _normalize_group_sparsities(group_sparsities, name=f"layer_{layer_idx}_group_sparsities")
+        raw_backend = backend_name or config_value(config, "sparse_attention_backend", "auto")
+        window_size = window_size or config_value(config, "sparse_attention_window_size", 512)
+        block_size = block_size or config_value(config, "sparse_attention_block_size", 64)
+        top_k = config_value(config, "sparse_attention_top_k", 128)
+        keep_ratio = config_value(config, "sparse_attention_keep_ratio", None)
+        groups = GroupSparsitySpec.build(group_sparsities, where=f"layer_{layer_idx}_group_sparsities").default
         if groups is None:
-            per_layer = _normalize_layer_group_sparsities(
-                _get_config_attr(config, "sparse_attention_layer_group_sparsities", None),
-                name="config.sparse_attention_layer_group_sparsities")
-            if per_layer is not None and layer_idx < len(per_layer):
-                groups = per_layer[layer_idx]
-        if groups is None:
-            groups = _normalize_group_sparsities(_get_config_attr(config, "sparse_attention_group_sparsities", None),
-                                                 name="config.sparse_attention_group_sparsities")
-        self.backend_candidates = _resolve_backend_candidates(pattern_name, raw_backend, keep_ratio, groups)
+            groups = GroupSparsitySpec.from_config(config).for_layer(layer_idx)
+        self.backend_candidates = backend_candidates(raw_backend)
         self.pattern_name = pattern_name
         self.backend_name = self.backend_candidates[0]
         self.window_size, self.block_size, self.top_k = window_size, block_size, top_k
@@ -99,10 +90,10 @@ class Qwen3SparseKernelAttention(Qwen3Attention):
         if self.pattern_name == "seeded_bigbird":
             return SeededBigBirdPattern(
                 rows=Hkv, block_size=self.block_size,
-                window=_get_config_attr(config, "sparse_attention_bigbird_window", 3),
-                global_blocks=_get_config_attr(config, "sparse_attention_bigbird_global", 2),
-                random_blocks=_get_config_attr(config, "sparse_attention_bigbird_random", 3),
-                seed=_get_config_attr(config, "sparse_attention_seed", 0) + layer_idx)
+                window=config_value(config, "sparse_attention_bigbird_window", 3),
+                global_blocks=config_value(config, "sparse_attention_bigbird_global", 2),
+                random_blocks=config_value(config, "sparse_attention_bigbird_random", 3),
+                seed=config_value(config, "sparse_attention_seed", 0) + layer_idx)
         if self.pattern_name == "dense":
             return DenseCausalPattern()
         if self.pattern_name == "local":
@@ -155,14 +146,13 @@ class Qwen3SparseKernelAttention(Qwen3Attention):
             k, v = cache.update(k, v, self.layer_idx, {"sin": sin, "cos": cos, "cache_position": cache_position})
         k_len = store.seq_len() if store is not None else k.size(2)
 
-        if self.validate_causal_mask and not _is_plain_causal_mask(attention_mask, q_len=q_len, k_len=k_len):
+        if self.validate_causal_mask and not is_plain_causal_mask(attention_mask, q_len=q_len, k_len=k_len):
             raise NotImplementedError("Sparse kernel path supports plain causal masks only; padding-aware or "
                                       "custom attention masks are not wired up.")
         # shape stand-in for the pattern when K/V live in pages (no data)
         k_like = k if store is None else q.new_empty((bsz, self.num_key_value_heads, k_len, 0))
         pattern = self.sparse_pattern.build(q, k_like, causal=True)
-        self.last_pattern_stats = (_compute_pattern_stats(pattern, q_len=q_len, k_len=k_len)
-                                   if self.collect_pattern_stats else None)
+        self.last_pattern_stats = pattern_stats(pattern) if self.collect_pattern_stats else None
         self.backend_name = self._select_backend(q, pattern)
         backend = self.sparse_backend = self.sparse_backends[self.backend_name]
 
@@ -209,46 +199,32 @@ def replace_qwen3_attention_with_sparse(model: nn.Module, *, backend_name: str =
     """Replaces every ``layer.self_attn`` of a Qwen3 decoder model (``:345-399``)."""
     if not hasattr(model, "layers"):
         raise TypeError("Expected a Qwen3 decoder model with a `.layers` attribute.")
-    groups = _normalize_group_sparsities(group_sparsities, name="group_sparsities")
-    if groups is None:
-        groups = _normalize_group_sparsities(_get_config_attr(model.config, "sparse_attention_group_sparsities", None),
-                                             name="config.sparse_attention_group_sparsities")
-    per_layer = _normalize_layer_group_sparsities(layer_group_sparsities, name="layer_group_sparsities")
-    if per_layer is None:
-        per_layer = _normalize_layer_group_sparsities(
-            _get_config_attr(model.config, "sparse_attention_layer_group_sparsities", None),
-            name="config.sparse_attention_layer_group_sparsities")
-    if per_layer is not None and len(per_layer) > len(model.layers):
+    spec = GroupSparsitySpec.from_config(model.config).overridden_by(
+        GroupSparsitySpec.build(group_sparsities, layer_group_sparsities))
+    if spec.per_layer is not None and len(spec.per_layer) > len(model.layers):
         raise ValueError("layer_group_sparsities has more entries than there are decoder layers.")
     for layer in model.layers:
-        idx = layer.self_attn.layer_idx
-        layer_groups = per_layer[idx] if per_layer is not None and idx < len(per_layer) else None
         layer.self_attn = build_sparse_attention_from_dense(
             layer.self_attn, backend_name=backend_name, window_size=window_size, block_size=block_size,
-            target_dtype=target_dtype, group_sparsities=layer_groups if layer_groups is not None else groups)
+            target_dtype=target_dtype, group_sparsities=spec.for_layer(layer.self_attn.layer_idx))
     return model
 
 
 def _apply_sparse_config_to_hf_config(config: Qwen3Config, *, group_sparsities=None,
                                       layer_group_sparsities=None) -> None:
-    _ensure_attn_implementation(config)
-    if group_sparsities is not None:
-        config.sparse_attention_group_sparsities = list(
-            _normalize_group_sparsities(group_sparsities, name="group_sparsities"))
-    if layer_group_sparsities is not None:
-        config.sparse_attention_layer_group_sparsities = _materialize_layer_group_sparsities(
-            _normalize_layer_group_sparsities(layer_group_sparsities, name="layer_group_sparsities"))
+    ensure_attn_implementation(config)
+    GroupSparsitySpec.build(group_sparsities, layer_group_sparsities).write_to(config)
 
 
 def _replace_sparse_attention_from_config(model: nn.Module, config: Qwen3Config) -> None:
     replace_qwen3_attention_with_sparse(
         model,
-        backend_name=_get_config_attr(config, "sparse_attention_backend", "hip_block_sparse"),
-        window_size=_get_config_attr(config, "sparse_attention_window_size", 512),
-        block_size=_get_config_attr(config, "sparse_attention_block_size", 64),
-        target_dtype=_get_config_attr(config, "sparse_attention_target_dtype", None),
-        group_sparsities=_get_config_attr(config, "sparse_attention_group_sparsities", None),
-        layer_group_sparsities=_get_config_attr(config, "sparse_attention_layer_group_sparsities", None))
+        backend_name=config_value(config, "sparse_attention_backend", "hip_block_sparse"),
+        window_size=config_value(config, "sparse_attention_window_size", 512),
+        block_size=config_value(config, "sparse_attention_block_size", 64),
+        target_dtype=config_value(config, "sparse_attention_target_dtype", None),
+        group_sparsities=config_value(config, "sparse_attention_group_sparsities", None),
+        layer_group_sparsities=config_value(config, "sparse_attention_layer_group_sparsities", None))
 
 
 class Qwen3SparseKernelModel(Qwen3Model):

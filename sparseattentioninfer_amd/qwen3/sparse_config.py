@@ -1,14 +1,24 @@
-"""Configuration helpers of the Qwen3 sparse-attention integration.
+"""Configuration of the Qwen3 sparse-attention integration.
 
-Same names and meaning as ``sparse_llm/qwen3/integrations/sparse_config.py``
-(``:13-219``), with the gfx950 backend in place of the Triton ones:
-``"auto"`` resolves to ``hip_block_sparse`` for every pattern, and
-:func:`validate_sparse_kernel_runtime` states that backend's conditions.
+The integration reads the reference's ``config.sparse_attention_*`` attributes
+(``sparse_llm/qwen3/integrations/sparse_config.py``).  This module organises them its own way:
+
+* :class:`GroupSparsitySpec` holds the per-KV-group sparsities of a model -- one default tuple
+  and optional per-layer overrides -- validates them once, resolves the precedence the
+  reference applies (explicit argument, then per-layer config, then model-wide config) in
+  :meth:`GroupSparsitySpec.for_layer`, writes them back to a config as JSON-friendly lists and
+  parses the command-line forms (``"0.5,0.7"``; a JSON list inline or in a file);
+* :func:`validate_sparse_kernel_runtime` (the reference's public check, ``:167-200``) states
+  the conditions of the gfx950 backend; ``"auto"`` resolves to that backend for every pattern;
+* :func:`is_plain_causal_mask`, :func:`describe_pattern` and :func:`pattern_stats` serve the
+  attention module.
+
 A ROCm GPU tensor reports ``device.type == "cuda"``.
 """
 from __future__ import annotations
 
 import json
+from dataclasses import dataclass
 from pathlib import Path
 from typing import Optional
 
@@ -18,112 +28,119 @@ KERNEL_BACKEND = "hip_block_sparse"
 SUPPORTED_BLOCK_SIZES = (16, 32, 64, 128)
 SUPPORTED_HEAD_DIMS = (64, 128)
 
+Sparsities = tuple[float, ...]
 
-def _get_config_attr(config, name: str, default):
+
+def config_value(config, name: str, default):
+    """``config.<name>``, or ``default`` where the config does not carry it."""
     return getattr(config, name, default)
 
 
-def _normalize_group_sparsities(values, *, name: str) -> Optional[tuple[float, ...]]:
-    """Tuple of floats in [0, 1), or None (``sparse_config.py:17-27``)."""
+def _as_sparsities(values, where: str) -> Optional[Sparsities]:
     if values is None:
         return None
-    normalized = tuple(float(v) for v in values)
-    if any(not 0.0 <= v < 1.0 for v in normalized):
-        raise ValueError(f"{name} values must satisfy 0 <= sparsity < 1.")
-    return normalized
+    out = tuple(float(x) for x in values)
+    outside = [x for x in out if not 0.0 <= x < 1.0]
+    if outside:
+        raise ValueError(f"{where} values must satisfy 0 <= sparsity < 1 (got {outside}).")
+    return out
 
 
-def _normalize_layer_group_sparsities(values, *, name: str):
-    """Per-layer group sparsities, entries may be None (``sparse_config.py:30-47``)."""
-    if values is None:
-        return None
-    return tuple(None if layer is None else _normalize_group_sparsities(layer, name=f"{name}[{i}]")
-                 for i, layer in enumerate(values))
+@dataclass(frozen=True)
+class GroupSparsitySpec:
+    """Per-KV-group sparsities: ``default`` for every layer, ``per_layer[i]`` (or None) for layer i."""
+
+    default: Optional[Sparsities] = None
+    per_layer: Optional[tuple[Optional[Sparsities], ...]] = None
+
+    @classmethod
+    def build(cls, default=None, per_layer=None, *, where: str = "group_sparsities") -> "GroupSparsitySpec":
+        layers = None
+        if per_layer is not None:
+            layers = tuple(None if entry is None else _as_sparsities(entry, f"layer_{where}[{i}]")
+                           for i, entry in enumerate(per_layer))
+        return cls(_as_sparsities(default, where), layers)
+
+    @classmethod
+    def from_config(cls, config) -> "GroupSparsitySpec":
+        return cls.build(config_value(config, "sparse_attention_group_sparsities", None),
+                         config_value(config, "sparse_attention_layer_group_sparsities", None),
+                         where="config.sparse_attention_group_sparsities")
+
+    def overridden_by(self, other: "GroupSparsitySpec") -> "GroupSparsitySpec":
+        """``other``'s entries where it has them, else this spec's."""
+        return GroupSparsitySpec(other.default if other.default is not None else self.default,
+                                 other.per_layer if other.per_layer is not None else self.per_layer)
+
+    def for_layer(self, layer_idx: int) -> Optional[Sparsities]:
+        if self.per_layer is not None and layer_idx < len(self.per_layer) \
+                and self.per_layer[layer_idx] is not None:
+            return self.per_layer[layer_idx]
+        return self.default
+
+    def write_to(self, config) -> None:
+        """Stores the spec on a config as plain lists (JSON-serialisable)."""
+        if self.default is not None:
+            config.sparse_attention_group_sparsities = list(self.default)
+        if self.per_layer is not None:
+            config.sparse_attention_layer_group_sparsities = [None if e is None else list(e) for e in self.per_layer]
+
+    @staticmethod
+    def parse_groups(text: Optional[str]) -> Optional[Sparsities]:
+        """Command-line form ``"0.5, 0.7"``; None or blank -> None."""
+        if text is None or not text.strip():
+            return None
+        return _as_sparsities([t for t in (p.strip() for p in text.split(",")) if t], "--group-sparsities")
+
+    @staticmethod
+    def parse_layers(text_or_path: Optional[str]) -> Optional[tuple[Optional[Sparsities], ...]]:
+        """A JSON list of per-layer lists (or nulls), inline or in a file."""
+        if text_or_path is None:
+            return None
+        src = Path(text_or_path)
+        doc = json.loads(src.read_text(encoding="utf-8") if src.is_file() else text_or_path)
+        if not isinstance(doc, list):
+            raise ValueError("--layer-group-sparsities must decode to a JSON list.")
+        return GroupSparsitySpec.build(None, doc, where="--layer-group-sparsities").per_layer
 
 
-def _materialize_layer_group_sparsities(values):
-    """JSON-friendly lists (``sparse_config.py:50-58``)."""
-    if values is None:
-        return None
-    return [None if layer is None else list(layer) for layer in values]
-
-
-def _parse_group_sparsities_arg(raw_value: Optional[str]) -> Optional[tuple[float, ...]]:
-    """``"0.5, 0.7"`` -> (0.5, 0.7); empty -> None (``sparse_config.py:61-70``)."""
-    if raw_value is None or not raw_value.strip():
-        return None
-    return _normalize_group_sparsities([c.strip() for c in raw_value.split(",") if c.strip()],
-                                       name="--group-sparsities")
-
-
-def _parse_layer_group_sparsities_arg(raw_value: Optional[str]):
-    """JSON list, given inline or as a file path (``sparse_config.py:73-89``)."""
-    if raw_value is None:
-        return None
-    path = Path(raw_value)
-    payload = path.read_text(encoding="utf-8") if path.is_file() else raw_value
-    parsed = json.loads(payload)
-    if not isinstance(parsed, list):
-        raise ValueError("--layer-group-sparsities must decode to a JSON list.")
-    return _normalize_layer_group_sparsities(parsed, name="--layer-group-sparsities")
-
-
-def _ensure_attn_implementation(config) -> None:
+def ensure_attn_implementation(config) -> None:
+    """Hugging Face needs an attention implementation name; the sparse layers replace it anyway."""
     if getattr(config, "_attn_implementation", None) is None:
         config._attn_implementation = "sdpa"
 
 
-def _resolve_backend_candidates(pattern_name: str, backend_name: str, keep_ratio: Optional[float] = None,
-                                group_sparsities=None) -> list[str]:
-    """Ordered backend names to try (``sparse_config.py:97-109``); "auto" -> the HIP kernel backend."""
-    if backend_name != "auto":
-        return [backend_name]
-    return [KERNEL_BACKEND]
+def backend_candidates(backend_name: str) -> list[str]:
+    """Backends a layer may use, in order: the named one, or the kernel backend for ``"auto"``."""
+    return [KERNEL_BACKEND] if backend_name == "auto" else [backend_name]
 
 
-def _resolve_backend_name(pattern_name: str, backend_name: str, keep_ratio: Optional[float] = None,
-                          group_sparsities=None) -> str:
-    return _resolve_backend_candidates(pattern_name, backend_name, keep_ratio, group_sparsities)[0]
+_DESCRIBED = ("top_k", "keep_ratio", "group_sparsities", "window_size", "window", "global_blocks",
+              "random_blocks", "block_size", "seed", "last_layout", "last_group_layouts")
 
 
-def _describe_pattern(attn) -> str:
-    """One-line description of a layer's pattern (``sparse_config.py:126-141``)."""
-    if attn.pattern_name == "bigbird":
-        if attn.group_sparsities is not None:
-            layouts = getattr(attn.sparse_pattern, "last_group_layouts", None)
-            resolved = f", layouts={layouts}" if layouts is not None else ""
-            return f"BigBirdGroupSparsity(group_sparsities={list(attn.group_sparsities)}{resolved})"
-        if attn.keep_ratio is not None:
-            layout = getattr(attn.sparse_pattern, "last_layout", None)
-            resolved = f", layout={layout}" if layout is not None else ""
-            return f"BigBirdKeepRatio(keep_ratio={attn.keep_ratio:.4f}{resolved})"
-        return f"BigBird(top_k={attn.top_k})"
-    if attn.pattern_name == "seeded_bigbird":
-        p = attn.sparse_pattern
-        return (f"SeededBigBird(window={p.window}, global={p.global_blocks}, random={p.random_blocks}, "
-                f"block_size={p.block_size}, seed={p.seed})")
-    if attn.pattern_name == "dense":
-        return "DenseCausal()"
-    return f"LocalWindow(window_size={attn.window_size}, block_size={attn.block_size})"
+def describe_pattern(attn) -> str:
+    """``PatternClass(field=value, ...)`` for the parameters a layer's pattern carries."""
+    p = attn.sparse_pattern
+    fields = ", ".join(f"{f}={getattr(p, f)}" for f in _DESCRIBED if getattr(p, f, None) is not None)
+    return f"{type(p).__name__}({fields})"
 
 
-def _is_plain_causal_mask(attention_mask: Optional[torch.Tensor], q_len: int, k_len: int) -> bool:
-    """True when the additive mask hides nothing a bottom-right causal mask keeps (``:144-164``)."""
+def is_plain_causal_mask(attention_mask: Optional[torch.Tensor], q_len: int, k_len: int) -> bool:
+    """Whether an attention mask hides nothing that the bottom-right aligned causal mask shows.
+
+    Accepts None, a 4-d additive float mask (negative = hidden) or a 4-d bool mask
+    (True = attend) of ``q_len`` rows and at least ``k_len`` columns.
+    """
     if attention_mask is None:
         return True
-    if attention_mask.dim() != 4:
+    m = attention_mask
+    if m.dim() != 4 or m.size(-2) != q_len or m.size(-1) < k_len:
         return False
-    if attention_mask.shape[-2] != q_len or attention_mask.shape[-1] < k_len:
-        return False
-    mask = attention_mask[..., :k_len]
-    q_pos = max(0, k_len - q_len) + torch.arange(q_len, device=mask.device)
-    k_pos = torch.arange(k_len, device=mask.device)
-    causal_keep = k_pos[None, :] <= q_pos[:, None]
-    if mask.dtype == torch.bool:     # boolean masks: True = attend
-        violations = (~mask) & causal_keep
-    else:
-        violations = (mask < 0) & causal_keep
-    return not bool(violations.any().item())
+    m = m[..., :k_len]
+    shown = torch.ones(q_len, k_len, dtype=torch.bool, device=m.device).tril(max(0, k_len - q_len))
+    hidden = ~m if m.dtype == torch.bool else m < 0
+    return not bool((hidden & shown).any())
 
 
 def validate_sparse_kernel_runtime(*, backend_name: str, device: torch.device, dtype: torch.dtype,
@@ -133,32 +150,29 @@ def validate_sparse_kernel_runtime(*, backend_name: str, device: torch.device, d
     """Whether the kernel backend can run these inputs, else the reason (``sparse_config.py:167-200``)."""
     if backend_name != KERNEL_BACKEND:
         return True, None
-    if device.type != "cuda":
-        return False, f"{backend_name} requires a ROCm GPU tensor; current device is {device.type}."
-    if dtype not in (torch.float16, torch.bfloat16):
-        return False, f"{backend_name} requires float16 or bfloat16 inputs; current dtype is {dtype}."
-    if head_dim is not None and head_dim not in SUPPORTED_HEAD_DIMS:
-        return False, f"{backend_name} supports head dims {SUPPORTED_HEAD_DIMS}; got {head_dim}."
-    if kind == "dense":
-        return True, None
-    if block_size is None:
-        return False, f"{backend_name} requires a block-sparse schedule; block_size is None."
-    if block_size not in SUPPORTED_BLOCK_SIZES:
-        return False, f"{backend_name} supports block sizes {SUPPORTED_BLOCK_SIZES}; got {block_size}."
+    checks = [
+        (device.type == "cuda", f"requires a ROCm GPU tensor; current device is {device.type}."),
+        (dtype in (torch.float16, torch.bfloat16), f"requires float16 or bfloat16 inputs; current dtype is {dtype}."),
+        (head_dim is None or head_dim in SUPPORTED_HEAD_DIMS, f"supports head dims {SUPPORTED_HEAD_DIMS}; got {head_dim}."),
+        (kind == "dense" or block_size is not None, "requires a block-sparse schedule; block_size is None."),
+        (kind == "dense" or block_size is None or block_size in SUPPORTED_BLOCK_SIZES,
+         f"supports block sizes {SUPPORTED_BLOCK_SIZES}; got {block_size}."),
+    ]
+    for ok, why in checks:
+        if not ok:
+            return False, f"{backend_name} {why}"
     return True, None
 
 
-def _compute_pattern_stats(pattern, q_len: int, k_len: int) -> dict[str, float]:
-    """Keep ratio / sparsity of a built pattern (``sparse_config.py:203-219``).
+def pattern_stats(pattern) -> dict[str, float]:
+    """Keep ratio and sparsity of a built pattern.
 
-    Block-scheduled patterns report their scheduled ratio without touching a
-    token mask (which may be lazy and large).
+    Block-scheduled patterns report their scheduled ratio; only a pattern with nothing but a
+    token mask has its ratio measured from the mask (a lazy mask would otherwise be built).
     """
-    stats = {"keep_ratio": float(pattern.keep_ratio), "sparsity": 1.0 - float(pattern.keep_ratio)}
-    if pattern.block_pairs is not None or pattern.kv_block_list is not None:
-        return stats
-    mask = pattern.mask
-    if mask is None:
-        return stats
-    exact = float(mask.float().mean().item())
-    return {"keep_ratio": exact, "sparsity": 1.0 - exact}
+    keep = float(pattern.keep_ratio)
+    scheduled = pattern.block_pairs is not None or pattern.kv_block_list is not None
+    if not scheduled and pattern.mask is not None:
+        keep = float(pattern.mask.float().mean().item())
+    return {"keep_ratio": keep, "sparsity": 1.0 - keep}
+

@@ -1,6 +1,7 @@
 """Callers of the backend on the CPU: KVCache / PagedKVStore semantics, AttentionLayer, and the Qwen3
 integration against Hugging Face's own eager Qwen3 (same weights, fp32)."""
 import copy
+from types import SimpleNamespace
 
 import pytest
 import torch
@@ -12,9 +13,8 @@ from sparseattentioninfer_amd.models import AttentionLayer, KVCache, PagedKVStor
 from sparseattentioninfer_amd.patterns import DenseCausalPattern, SeededBigBirdPattern
 from sparseattentioninfer_amd.qwen3 import PagedKVCache, replace_qwen3_attention_with_sparse
 from sparseattentioninfer_amd.qwen3.runtime import qwen3_config
-from sparseattentioninfer_amd.qwen3.sparse_config import (_is_plain_causal_mask, _parse_group_sparsities_arg,
-                                                          _resolve_backend_candidates,
-                                                          validate_sparse_kernel_runtime)
+from sparseattentioninfer_amd.qwen3.sparse_config import (GroupSparsitySpec, backend_candidates,
+                                                          is_plain_causal_mask, validate_sparse_kernel_runtime)
 from tests import oracle_backend
 
 ORACLE = oracle_backend.register()
@@ -167,11 +167,11 @@ def test_qwen3_sparse_layers_selection_and_pattern_stats():
 
 
 def test_qwen3_config_helpers():
-    assert _resolve_backend_candidates("bigbird", "auto") == ["hip_block_sparse"]
-    assert _resolve_backend_candidates("local", "x") == ["x"]
-    assert _parse_group_sparsities_arg(" 0.5, 0.75 ") == (0.5, 0.75)
+    assert backend_candidates("auto") == ["hip_block_sparse"]
+    assert backend_candidates("x") == ["x"]
+    assert GroupSparsitySpec.parse_groups(" 0.5, 0.75 ") == (0.5, 0.75)
     with pytest.raises(ValueError):
-        _parse_group_sparsities_arg("1.0")
+        GroupSparsitySpec.parse_groups("1.0")
     ok, why = validate_sparse_kernel_runtime(backend_name="hip_block_sparse", device=torch.device("cpu"),
                                              dtype=torch.bfloat16, block_size=64)
     assert not ok and "ROCm GPU" in why
@@ -184,13 +184,38 @@ def test_qwen3_config_helpers():
     causal = torch.zeros(1, 1, 3, 5)
     causal[..., 0, 3:] = float("-inf")
     causal[..., 1, 4:] = float("-inf")
-    assert _is_plain_causal_mask(causal, 3, 5) and _is_plain_causal_mask(None, 3, 5)
+    assert is_plain_causal_mask(causal, 3, 5) and is_plain_causal_mask(None, 3, 5)
     causal[..., 2, 0] = float("-inf")   # padding hides a causally visible key
-    assert not _is_plain_causal_mask(causal, 3, 5)
+    assert not is_plain_causal_mask(causal, 3, 5)
 
 
 def test_hip_backend_refuses_cpu_tensors():
     from sparseattentioninfer_amd.attention import get_backend
     x = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16)
-    with pytest.raises(RuntimeError, match="no CPU fallback"):
+    with pytest.raises(RuntimeError, match="no fallback backend was given"):
         get_backend("hip_block_sparse").forward(x, x, x, DenseCausalPattern().build(x, x))
+
+
+def test_group_sparsity_spec_precedence_and_parsing(tmp_path):
+    cfg = qwen3_config(pattern="bigbird", vocab_size=97, hidden_size=64, intermediate_size=128,
+                       num_hidden_layers=3, num_attention_heads=4, num_key_value_heads=2, head_dim=16)
+    cfg.sparse_attention_group_sparsities = [0.5, 0.6]
+    cfg.sparse_attention_layer_group_sparsities = [None, [0.7, 0.8]]
+    spec = GroupSparsitySpec.from_config(cfg)
+    assert spec.for_layer(0) == (0.5, 0.6) and spec.for_layer(1) == (0.7, 0.8) and spec.for_layer(2) == (0.5, 0.6)
+    arg = GroupSparsitySpec.build([0.1, 0.2])                      # explicit default wins over the config's
+    merged = spec.overridden_by(arg)
+    assert merged.for_layer(0) == (0.1, 0.2) and merged.for_layer(1) == (0.7, 0.8)
+    path = tmp_path / "layers.json"
+    path.write_text("[[0.25], null]")
+    assert GroupSparsitySpec.parse_layers(str(path)) == ((0.25,), None)
+    assert GroupSparsitySpec.parse_layers("[null, [0.5]]") == (None, (0.5,))
+    assert GroupSparsitySpec.parse_groups("  ") is None
+    with pytest.raises(ValueError, match="JSON list"):
+        GroupSparsitySpec.parse_layers('{"a": 1}')
+    with pytest.raises(ValueError, match="0 <= sparsity < 1"):
+        GroupSparsitySpec.build(None, [[0.5], [-0.1]])
+    out = SimpleNamespace()
+    merged.write_to(out)
+    assert out.sparse_attention_group_sparsities == [0.1, 0.2]
+    assert out.sparse_attention_layer_group_sparsities == [None, [0.7, 0.8]]
