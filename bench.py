@@ -7,7 +7,9 @@ Qwen3-4B attention shape (configs[2]: B=1, 32 query / 8 KV heads, head dim
 counts (0,1,2,3,3,4,6,8) per KV group), counting retained blocks only
 (4 * 64 * 64 * 128 FLOP per retained (query head, query block, key block)).
 
-Also reported (``decode``): the paged sparse decode of configs[3] (B=64
+Also reported (``configs1``): the arbitrary-pattern prefill of configs[1] (B=4,
+32 query / 8 KV heads, 8192 tokens, a seeded Bernoulli(0.10) block mask per KV
+group), same units.  (``decode``): the paged sparse decode of configs[3] (B=64
 sequences, 16384 cached tokens each in 64-token pages, 14 retained blocks per
 (sequence, KV head)) in tokens/s and HBM GB/s; and ``cpu_baseline``: the
 dense-masked PyTorch path (the reference's ``MaskedSdpaBackend`` arithmetic,
@@ -52,7 +54,7 @@ def parse():
     # The shader clock ramps up over the first tens of milliseconds of sustained load; the
     # default warm-up (about 0.1 s of prefill) lets timing start at steady clocks.
     ap.add_argument("--warmup", type=int, default=200)
-    ap.add_argument("--only", choices=("all", "prefill", "decode"), default="all",
+    ap.add_argument("--only", choices=("all", "prefill", "bernoulli", "decode"), default="all",
                     help="restrict to one kernel (for profiler runs)")
     ap.add_argument("--decode-splits", type=int, default=0, help="0 = time 1 and 2, keep the faster")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
@@ -130,6 +132,45 @@ def run_prefill(args, dev):
         "tensors": (q, k, v, bm),
     }
     return res
+
+
+def bernoulli_workload(dev):
+    """B=4, 32Q/8KV, D=128, T=8192, an independent seeded Bernoulli(0.10) block mask per
+    KV group over the causal lower triangle with the diagonal kept; q, k, v ~ N(0, 1)."""
+    import torch
+    from sparseattentioninfer_amd.patterns import bernoulli_block_mask, block_mask_to_csr
+    B, T, Hq, Hkv, D = 4, 8192, 32, 8, 128
+    g = torch.Generator(device=dev).manual_seed(3031)
+    q = torch.randn(B, Hq, T, D, generator=g, device=dev).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, T, D, generator=g, device=dev).to(torch.bfloat16)
+    nqb = T // BS
+    bm = bernoulli_block_mask(Hkv, nqb, nqb, density=0.10, seed=17)
+    pairs, offsets = block_mask_to_csr(bm)
+    nnz_group = bm.sum(dim=(1, 2))
+    causal_blocks = nqb * (nqb + 1) // 2
+    info = {
+        "workload": "configs[1] arbitrary-pattern (Bernoulli 10%) block-sparse causal prefill",
+        "batch": B, "seq_len": T, "q_heads": Hq, "kv_heads": Hkv, "head_dim": D, "block": BS,
+        "pattern": "seeded Bernoulli(0.10) per KV group over the causal lower triangle, diagonal kept",
+        "csr_rows": "per KV group (shared by its 4 query heads and the batch)",
+        "retained_pairs": int(nnz_group.sum().item()) * (Hq // Hkv) * B,
+        "group_density": [round(x / causal_blocks, 4) for x in nnz_group.tolist()],
+    }
+    flops = info["retained_pairs"] * PAIR_FLOP * D
+    return (q, k, v, pairs.to(dev), offsets.to(dev)), info, flops
+
+
+def run_prefill_bernoulli(args, dev):
+    from sparseattentioninfer_amd import ops
+    (q, k, v, pairs, offsets), info, flops = bernoulli_workload(dev)
+    launch = ops.prepare_prefill(q, k, v, pairs, offsets, BS)
+    wall, ev = _events_time(launch, args.steps, args.warmup)
+    avg = ev / args.steps
+    return {**info, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3,
+            "kernel_us": avg * 1e6, "tflops": flops / (wall / args.steps) / 1e12, "flops_per_launch": flops,
+            "roofline": {"bound": "mfma", "achieved": flops / avg / 1e12, "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None}}
 
 
 def decode_workload(dev):
@@ -265,6 +306,50 @@ def copy_calibration(dev):
     print(json.dumps({"copy_bytes": n, "note": "3 device copies of 1 GiB; compare FETCH_SIZE/WRITE_SIZE"}))
 
 
+def _attach_traffic(line: dict, prefill_first: bool) -> None:
+    """``roofline.traffic`` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of each
+    kernel (``profiles/traffic.json``), labelled with the summary it came from and the source
+    commit of the kernel it measured.  The counters cannot be read inside this process; a kernel
+    whose source changed after its summary was taken gets null instead of a stale figure."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return
+    try:
+        table = json.loads(path.read_text())
+    except ValueError:
+        return
+    current = _kernel_source_digest()
+
+    def put(roof: dict, key: str) -> None:
+        entry = table.get(key)
+        if not entry or roof is None:
+            return
+        if entry.get("kernel_source_sha1") != current.get(entry.get("kernel_source")):
+            roof["traffic"] = None
+            roof["traffic_source"] = f"{entry.get('summary')}: taken for an older {entry.get('kernel_source')}; null"
+            return
+        roof["traffic"] = entry["hbm_bytes_per_launch"]
+        roof["traffic_source"] = f"{entry.get('summary')} (rocprofv3 --pmc, calibrated; not measured in this run)"
+
+    if "roofline" in line and prefill_first:
+        put(line["roofline"], "prefill_cfg2")
+    if "configs1" in line:
+        put(line["configs1"]["roofline"], "prefill_cfg1")
+    if "decode" in line:
+        put(line["decode"]["roofline"], "decode_cfg3")
+        if not prefill_first and "roofline" in line:
+            put(line["roofline"], "decode_cfg3")
+
+
+def _kernel_source_digest() -> dict:
+    """sha1 of each HIP source file, so a traffic figure is used only for the kernel it measured."""
+    import hashlib
+    out = {}
+    for f in (ROOT / "sparseattentioninfer_amd" / "csrc").glob("*.hip"):
+        out[f.name] = hashlib.sha1(f.read_bytes()).hexdigest()
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -292,6 +377,14 @@ def main():
         line["config"] = {**pre["info"], "kernel_us": round(pre["kernel_us"], 2),
                           "flops_per_launch": pre["flops_per_launch"]}
         line["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre["roofline"].items()}
+    if args.only in ("all", "bernoulli"):
+        c1 = run_prefill_bernoulli(args, dev)
+        c1["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c1["roofline"].items()}
+        line["configs1"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c1.items()}
+        if pre is None and args.only == "bernoulli":
+            line.update(value=round(c1["tflops"], 3), ms_per_step=round(c1["ms_per_step"], 4),
+                        config={"workload": c1["workload"], "kernel_us": round(c1["kernel_us"], 2)},
+                        roofline=line["configs1"]["roofline"])
     if args.only in ("all", "decode"):
         dec = run_decode(args, dev)
         dec["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()}
@@ -310,17 +403,7 @@ def main():
         cb = cpu_baseline(pre, args.cpu_seconds)
         cb["value"] = round(cb["value"], 5)
         line["cpu_baseline"] = cb
-    traffic = ROOT / "profiles" / "traffic.json"
-    if traffic.exists() and "roofline" in line:
-        try:
-            t = json.loads(traffic.read_text())
-            key = "prefill" if pre is not None else "decode"
-            if key in t:
-                line["roofline"]["traffic"] = t[key]["hbm_bytes_per_launch"]
-            if "decode" in line and "decode" in t:
-                line["decode"]["roofline"]["traffic"] = t["decode"]["hbm_bytes_per_launch"]
-        except (ValueError, KeyError):
-            pass
+    _attach_traffic(line, pre is not None)
     print(json.dumps(line), flush=True)
 
 

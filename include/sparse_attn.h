@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 3
+#define SA_ABI_VERSION 4
 
 /* element types */
 #define SA_DTYPE_BF16 0
@@ -160,7 +160,11 @@ int sa_csr_to_tiles(const int32_t* pairs, int64_t pairs_stride,
  *                                      + g*kv_sh + (t % page)*kv_st
  *   contiguous (block_table == NULL): base + b*kv_sb + g*kv_sh + t*kv_st
  * where t = lb*page + i.  K and V share strides.  kv_lens[b] (or kv_len for
- * every sequence when kv_lens == NULL) is the number of valid tokens.
+ * every sequence when kv_lens == NULL) is the number of valid tokens.  A paged
+ * block_table has max_blocks columns (row stride bt_stride >= max_blocks) over
+ * pools of num_pages pages: a retained block at or past max_blocks, or whose
+ * page lies outside [0, num_pages), is skipped (it contributes no keys), so a
+ * kv_len beyond the table or a corrupt page id is never read out of bounds.
  *
  * Retained blocks of (b, row): sel[b*sel_sb + row*sel_sr + i] for
  * i in [sel_off[b*off_sb + row*off_sr], sel_off[b*off_sb + row*off_sr + 1]);
@@ -176,7 +180,7 @@ int sa_decode(int dtype,
               const void* q, int64_t q_sb, int64_t q_sh,
               const void* k, const void* v,
               int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
-              const int32_t* block_table, int64_t bt_stride,
+              const int32_t* block_table, int64_t bt_stride, int max_blocks, int num_pages,
               const int32_t* kv_lens, int kv_len,
               const int32_t* sel, int64_t sel_sb, int64_t sel_sr,
               const int32_t* sel_off, int64_t off_sb, int64_t off_sr,

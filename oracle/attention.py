@@ -88,6 +88,46 @@ def masked_sdpa_rows(q_rows: torch.Tensor, k: torch.Tensor, v: torch.Tensor, kee
     return torch.matmul(attn, v)
 
 
+def masked_sdpa_blockwise(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_mask: torch.Tensor,
+                          block_size: int, q_offset: int | None = None, row_chunk: int = 1024) -> torch.Tensor:
+    """:func:`masked_sdpa` over a block-level keep mask, in chunks of query rows, on q's device.
+
+    The reference's dense-masked arithmetic (``masked_sdpa.py:35-68``: full scores against
+    every key, ``-inf`` outside the keep mask AND the causal mask, softmax, NaN rows -> 0,
+    times V), evaluated ``row_chunk`` query rows at a time so that workloads whose
+    ``[H, T_q, T_k]`` score tensor cannot be held at once (32 K tokens) are still checked
+    exhaustively.  ``q [B,Hq,T_q,D]``, ``k, v [B,Hkv,T_k,D]``; ``block_mask [R, NQB, NKB]``
+    bool with ``R = Hq`` (per query head) or ``R = Hkv`` (per KV group); query row ``t`` sits
+    at absolute position ``q_offset + t`` (default ``T_k - T_q``).  Computes in fp32.
+    """
+    B, Hq, T_q, D = q.shape
+    Hkv, T_k = k.shape[1], k.shape[2]
+    if q_offset is None:
+        q_offset = T_k - T_q
+    R = block_mask.shape[0]
+    rowmap = _row_head_map(Hq, R)
+    bs = block_size
+    dev = q.device
+    bm = block_mask.to(dev)
+    out = torch.empty(B, Hq, T_q, D, dtype=torch.float32, device=dev)
+    kpos = torch.arange(T_k, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    for h in range(Hq):
+        g = h // (Hq // Hkv)
+        kt = k[:, g].float().transpose(1, 2).contiguous()            # [B, D, T_k]
+        vg = v[:, g].float()
+        for r0 in range(0, T_q, row_chunk):
+            r1 = min(T_q, r0 + row_chunk)
+            rows = torch.arange(r0, r1, device=dev)
+            keep = bm[int(rowmap[h])][rows // bs].repeat_interleave(bs, dim=1)[:, :T_k]
+            keep = keep & (kpos[None, :] <= (q_offset + rows)[:, None])
+            scores = torch.matmul(q[:, h, r0:r1].float(), kt) * scale
+            scores = scores.masked_fill(~keep[None], float("-inf"))
+            attn = torch.nan_to_num(F.softmax(scores, dim=-1), nan=0.0)
+            out[:, h, r0:r1] = torch.matmul(attn, vg)
+    return out
+
+
 def textbook_attention(q, k, v, keep) -> np.ndarray:
     """float64 loop definition: ``out[i] = sum_j softmax_j(q_i.k_j / sqrt(D))[keep] v_j``.
 
@@ -202,7 +242,7 @@ def block_sparse_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pa
 
 
 def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.Tensor,
-                           block_table, kv_lens, sel, sel_offsets) -> torch.Tensor:
+                           block_table, kv_lens, sel, sel_offsets, device="cpu") -> torch.Tensor:
     """One decode token per sequence over a paged cache, fp32.
 
     ``q [B, Hq, D]``; pools ``[P, Hkv, page, D]``; ``block_table [B, max_blocks]``
@@ -210,7 +250,8 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
     ``(b, row)`` are ``sel[b, row, sel_offsets[b,row,0]:sel_offsets[b,row,1]]``
     with rows = Hkv (group-shared) or Hq.  The query is the newest token, so
     every cached key of a retained block below ``kv_lens[b]`` is visible
-    (``masked_sdpa.py:42-46``, decode row of the causal mask).
+    (``masked_sdpa.py:42-46``, decode row of the causal mask).  Computes on ``device``
+    (the page pools are read where they are, only the retained pages are moved).
     """
     B, Hq, D = q.shape
     Hkv, page = k_pages.shape[1], k_pages.shape[2]
@@ -220,11 +261,10 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
     block_table = np.asarray(block_table)
     kv_lens = np.asarray(kv_lens)
     R = sel_offsets.shape[1]
-    out = torch.zeros(B, Hq, D, dtype=torch.float32)
+    out = torch.zeros(B, Hq, D, dtype=torch.float32, device=device)
     scale = 1.0 / math.sqrt(D)
-    kp = k_pages.float().cpu()
-    vp = v_pages.float().cpu()
-    qf = q.float().cpu()
+    kp, vp = k_pages, v_pages
+    qf = q.float().to(device)
     for b in range(B):
         L = int(kv_lens[b])
         for h in range(Hq):
@@ -237,8 +277,8 @@ def paged_decode_attention(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torc
                 if n <= 0:
                     continue
                 pg = int(block_table[b, int(lb)])
-                ks.append(kp[pg, kvh, :n])
-                vs.append(vp[pg, kvh, :n])
+                ks.append(kp[pg, kvh, :n].to(device).float())
+                vs.append(vp[pg, kvh, :n].to(device).float())
             if not ks:
                 continue
             K = torch.cat(ks)

@@ -11,7 +11,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 
@@ -61,7 +61,7 @@ SIGNATURES = {
         _vp, _i64, _i64,
         _vp, _vp,
         _i64, _i64, _i64,
-        _vp, _i64,
+        _vp, _i64, _i32, _i32,
         _vp, _i32,
         _vp, _i64, _i64,
         _vp, _i64, _i64,

@@ -27,6 +27,8 @@ struct DecodeArgs {
   int64_t kv_sb, kv_sh, kv_st;
   const int32_t* block_table;
   int64_t bt_stride;
+  int max_blocks;  // columns of block_table
+  int num_pages;   // pages in each pool
   const int32_t* kv_lens;
   int kv_len;
   const int32_t* sel;
@@ -62,6 +64,15 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
+// Page of logical block lb of sequence b in a paged cache, or -1 where the block has no keys
+// below L, lies past the table's max_blocks columns, or maps outside the pool: such blocks load
+// nothing.
+__device__ __forceinline__ int page_of(const DecodeArgs& a, int b, int lb, int L) {
+  if (lb < 0 || lb >= a.max_blocks || (int64_t)lb * a.page >= L) return -1;
+  const int pg = a.block_table[b * a.bt_stride + lb];
+  return (pg >= 0 && pg < a.num_pages) ? pg : -1;
+}
+
 template <bool BF16, int D, int NH>
 struct Decode {
   using E = Elem<BF16>;
@@ -94,7 +105,10 @@ struct Decode {
       pg = c.s_pg[x];
     } else {
       lb = c.selp[c.lo + x];
-      if (a.block_table && lb >= 0 && (int64_t)lb * a.page < c.L) pg = a.block_table[c.b * a.bt_stride + lb];
+      if (a.block_table) {
+        pg = page_of(a, c.b, lb, c.L);
+        if (pg < 0) lb = -1;
+      }
     }
     lb = __builtin_amdgcn_readfirstlane(lb);
     pg = __builtin_amdgcn_readfirstlane(pg);
@@ -218,9 +232,12 @@ struct Decode {
     // Stage the list (and its pages) once: the round loop then reads LDS, not dependent HBM loads.
     if (c.cached)
       for (int x = tid; x < nsel; x += 64 * DEC_WAVES) {
-        const int lb = c.selp[c.lo + x];
+        int lb = c.selp[c.lo + x];
         int pg = 0;
-        if (a.block_table && lb >= 0 && (int64_t)lb * a.page < c.L) pg = a.block_table[b * a.bt_stride + lb];
+        if (a.block_table) {
+          pg = page_of(a, b, lb, c.L);
+          if (pg < 0) lb = -1;
+        }
         s_blk[x] = lb;
         s_pg[x] = pg;
       }
@@ -387,7 +404,7 @@ extern "C" int sa_decode(int dtype,
                          const void* q, int64_t q_sb, int64_t q_sh,
                          const void* k, const void* v,
                          int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
-                         const int32_t* block_table, int64_t bt_stride,
+                         const int32_t* block_table, int64_t bt_stride, int max_blocks, int num_pages,
                          const int32_t* kv_lens, int kv_len,
                          const int32_t* sel, int64_t sel_sb, int64_t sel_sr,
                          const int32_t* sel_off, int64_t off_sb, int64_t off_sr,
@@ -413,6 +430,9 @@ extern "C" int sa_decode(int dtype,
   if (!q || !k || !v || !o || !sel || !sel_off)
     return set_error(SA_E_NULL, "sa_decode: NULL pointer argument");
   if (!kv_lens && kv_len < 0) return set_error(SA_E_SHAPE, "sa_decode: kv_len=%d < 0", kv_len);
+  if (block_table && (max_blocks < 0 || num_pages < 0 || bt_stride < max_blocks))
+    return set_error(SA_E_SHAPE, "sa_decode: block table of %d columns (row stride %lld) over %d pages", max_blocks,
+                     (long long)bt_stride, num_pages);
   const int64_t strides[] = {q_sb, q_sh, kv_sb, kv_sh, kv_st};
   for (int64_t s : strides)
     if (s % 8) return set_error(SA_E_ALIGN, "sa_decode: stride %lld is not a multiple of 8 elements", (long long)s);
@@ -429,6 +449,7 @@ extern "C" int sa_decode(int dtype,
   a.v = static_cast<const elem_t*>(v);
   a.kv_sb = kv_sb; a.kv_sh = kv_sh; a.kv_st = kv_st;
   a.block_table = block_table; a.bt_stride = bt_stride;
+  a.max_blocks = max_blocks; a.num_pages = num_pages;
   a.kv_lens = kv_lens; a.kv_len = kv_len;
   a.sel = sel; a.sel_sb = sel_sb; a.sel_sr = sel_sr;
   a.sel_off = sel_off; a.off_sb = off_sb; a.off_sr = off_sr;

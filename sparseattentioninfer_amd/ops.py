@@ -201,7 +201,7 @@ def universal_sparse_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
             q.data_ptr(), q.stride(0), q.stride(1),
             k.data_ptr(), v.data_ptr(),
             *_kv_strides(k, v, name),
-            None, 0, None, T_k,
+            None, 0, 0, 0, None, T_k,
             pairs.data_ptr(), 0, pairs.stride(0),
             offsets.data_ptr(), 0, offsets.stride(0),
             R,
@@ -287,6 +287,9 @@ def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.T
     for t in (block_table, kv_lens, sel, sel_off):
         _require(t.dtype == torch.int32 and t.device == q3.device, f"{name}: index tensors must be int32 on the GPU")
     _require(sel.dim() == 3 and sel_off.dim() == 3 and sel_off.shape[2] == 2, f"{name}: bad sel shapes")
+    _require(block_table.dim() == 2 and block_table.size(0) == B,
+             f"{name}: block_table must be [B={B}, max_blocks], got {tuple(block_table.shape)}")
+    _require(kv_lens.shape == (B,), f"{name}: kv_lens must be [B={B}], got {tuple(kv_lens.shape)}")
     R = sel.shape[1]
     _require(R in (Hq, Hkv) and sel_off.shape[:2] == (B, R) and sel.shape[0] == B, f"{name}: bad sel rows")
     _require(sel.stride(2) == 1 and block_table.stride(1) == 1 and kv_lens.is_contiguous()
@@ -306,7 +309,7 @@ def paged_sparse_decode(q: torch.Tensor, k_pages: torch.Tensor, v_pages: torch.T
         q3.data_ptr(), q3.stride(0), q3.stride(1),
         k_pages.data_ptr(), v_pages.data_ptr(),
         *_kv_strides(k_pages, v_pages, name),
-        block_table.data_ptr(), block_table.stride(0),
+        block_table.data_ptr(), block_table.stride(0), block_table.size(1), k_pages.size(0),
         kv_lens.data_ptr(), 0,
         sel.data_ptr(), sel.stride(0), sel.stride(1),
         sel_off.data_ptr(), sel_off.stride(0), sel_off.stride(1),
@@ -388,7 +391,7 @@ def prepare_paged_decode(q, k_pages, v_pages, block_table, kv_lens, sel, sel_off
         _DTYPES[q3.dtype],
         q3.data_ptr(), q3.stride(0), q3.stride(1),
         k_pages.data_ptr(), v_pages.data_ptr(), k_pages.stride(0), k_pages.stride(1), k_pages.stride(2),
-        block_table.data_ptr(), block_table.stride(0), kv_lens.data_ptr(), 0,
+        block_table.data_ptr(), block_table.stride(0), block_table.size(1), k_pages.size(0), kv_lens.data_ptr(), 0,
         sel.data_ptr(), sel.stride(0), sel.stride(1), sel_off.data_ptr(), sel_off.stride(0), sel_off.stride(1),
         sel.shape[1], out.data_ptr(), out.stride(0), out.stride(1),
         B, Hq, Hkv, D, page, 1.0 / math.sqrt(D),

@@ -13,11 +13,16 @@ and replays it for every token.
 Everything that changes from token to token lives on the device, so one
 capture serves every step: the position, the token ids, ``kv_lens``, the page
 and slot of the paged write, and each layer's decode block selection.  The
-selection of a decode step depends only on its query block ``qb = pos // page``
-(the reference's decode row, ``sparse_attentions/patterns/bigbird_pattern.py:236,246``);
-the decoder builds it for every ``qb`` the run can reach with the layer's own
-pattern (``pattern.build`` and the backend's schedule, exactly as the eager
-path does per step) and gathers row ``qb`` on the device.
+selection of a step is whatever the layer's own pattern and the backend's
+schedule give for that step's key length (``pattern.build`` at ``T_k = pos + 1``,
+exactly as the eager path does per step).  BigBird selections change only at
+page boundaries (the reference's decode row ``qb = (T_k - 1) // bs``,
+``sparse_attentions/patterns/bigbird_pattern.py:236,246``), but a local window
+whose length is not a multiple of the page moves inside a page, and keep-ratio
+layouts take their budget from ``T_k``.  So the decoder builds the selection of
+every position the run can reach, keeps the distinct combinations of all
+layers' selections in one table, and a step gathers its row through a
+per-position index on the device.
 
 With ``fused=True`` (the default) a layer is eight launches: one GEMM for the
 concatenated q|k|v projection (``sa_gemm_skinny``, which streams the weights
@@ -59,18 +64,29 @@ def _argmax_chunk(V: int) -> int:
 
 
 class _LayerSchedule:
-    """Decode block selections of one layer for query blocks ``qb0 .. qb1`` (device tables)."""
+    """Decode block selections of one layer for every position ``pos0 .. pos1 - 1``.
 
-    def __init__(self, attn, store, qb0: int, qb1: int, batch: int, device):
+    ``table [n_rows, R, width]`` / ``counts [n_rows, R]`` hold the distinct selections in
+    order of first use and ``row_of[p - pos0]`` the row of position ``p``.  A schedule the
+    pattern returns again as the same tensors (its cache) is not read again; a new one is
+    compared with the previous row, so runs of equal selections share one row.
+    """
+
+    def __init__(self, attn, store, pos0: int, pos1: int, batch: int, device):
         page, H, D = store.page, attn.num_heads, attn.head_dim
         backend = attn.sparse_backend
-        rows, counts = [], []
-        for qb in range(qb0, qb1 + 1):
-            T_k = qb * page + 1
-            q_like = torch.empty(batch, H, 1, 0, device=device)
+        rows, counts, row_of = [], [], []
+        last_src = None        # (pairs, offsets) of the previous position, kept alive for the identity test
+        q_like = torch.empty(batch, H, 1, 0, device=device)
+        for pos in range(pos0, pos1):
+            T_k = pos + 1
             k_like = torch.empty(batch, attn.num_key_value_heads, T_k, 0, device=device)
             pattern = attn.sparse_pattern.build(q_like, k_like, causal=True)
             pairs, offsets, bs = backend._schedule(1, T_k, attn.num_key_value_heads, device, pattern)
+            if last_src is not None and pairs is last_src[0] and offsets is last_src[1]:
+                row_of.append(len(rows) - 1)
+                continue
+            last_src = (pairs, offsets)
             if bs != page:
                 raise ValueError(f"layer {attn.layer_idx}: schedule block {bs} differs from the page {page}")
             if offsets.size(1) != 2:
@@ -82,14 +98,20 @@ class _LayerSchedule:
             idx = start[:, None] + torch.arange(width, device=pairs.device)[None, :]
             ok = torch.arange(width, device=pairs.device)[None, :] < cnt[:, None]
             row = torch.where(ok, pairs.gather(1, idx.clamp(max=pairs.size(1) - 1)), torch.zeros_like(idx))
-            rows.append(row.to(torch.int32))
-            counts.append(cnt.to(torch.int32))
+            row, cnt = row.to(torch.int32), cnt.to(torch.int32)
+            if rows and rows[-1].shape == row.shape and torch.equal(rows[-1], row) and torch.equal(counts[-1], cnt):
+                row_of.append(len(rows) - 1)
+                continue
+            rows.append(row)
+            counts.append(cnt)
+            row_of.append(len(rows) - 1)
         R = rows[0].size(0)
         self.width = max(r.size(1) for r in rows)
         self.table = torch.zeros(len(rows), R, self.width, dtype=torch.int32, device=device)
         for i, r in enumerate(rows):
             self.table[i, :, :r.size(1)] = r
-        self.counts = torch.stack(counts).to(device)              # [n_qb, R]
+        self.counts = torch.stack(counts).to(device)              # [n_rows, R]
+        self.row_of = row_of
         self.sel = self.sel_off = None  # views of the decoder's gathered selections (set by the decoder)
         self.rows = R
         self.num_splits = ops.auto_decode_splits(batch, R, self.width)
@@ -136,15 +158,13 @@ class GraphDecoder:
             if not hasattr(layer.self_attn.sparse_backend, "forward_paged"):
                 raise ValueError("GraphDecoder needs a backend with paged decode (hip_block_sparse)")
         # one selection table per distinct pattern (dense causal layers all share one)
-        qb0, qb1 = self.start // self.page, (max_len - 1) // self.page
-        self.qb0 = qb0
         sched: dict = {}
         self.sched = []
         for layer, store in zip(self.layers, self.stores):
             attn = layer.self_attn
             key = "dense" if attn.pattern_name == "dense" else id(attn.sparse_pattern)
             if key not in sched:
-                sched[key] = _LayerSchedule(attn, store, qb0, qb1, self.B, self.dev)
+                sched[key] = _LayerSchedule(attn, store, self.start, max_len, self.B, self.dev)
             self.sched.append(sched[key])
         self.uniq_sched = list(sched.values())
         self._merge_selections()
@@ -205,9 +225,8 @@ class GraphDecoder:
         L = len(self.layers)
         self.h.copy_(m.embed_tokens(self.ids))
         ops.rmsnorm(self.h, self.layers[0].input_layernorm.weight, self.eps, out=self.x)
-        qb_rel = torch.div(self.pos, self.page, rounding_mode="floor") - self.qb0
         self.kv_lens.copy_((self.pos + 1).to(torch.int32).expand(self.B))
-        self._select(qb_rel)
+        self._select()
         B = self.B
         # Every projection on the skinny GEMM (the down projection on hipBLASLt when its K, the
         # intermediate size, is past the skinny kernel's limit).
@@ -237,28 +256,37 @@ class GraphDecoder:
         self.pos.add_(1)
 
     def _merge_selections(self) -> None:
-        """Stacks every schedule's selection table into one, so that a step gathers the selections of
-        all layers with two launches; each schedule's ``sel`` / ``sel_off`` become views of the
-        gathered buffers (the decode kernel takes their row strides)."""
+        """Stacks the distinct combinations of every schedule's selection (one per position the run
+        reaches, deduplicated) into one table, so that a step gathers the selections of all layers
+        with three launches (position -> combination, then the two tables); each schedule's
+        ``sel`` / ``sel_off`` become views of the gathered buffers (the decode kernel takes their
+        row strides)."""
         S = len(self.uniq_sched)
         R = max(s.rows for s in self.uniq_sched)
         W = max(s.width for s in self.uniq_sched)
-        nqb = self.uniq_sched[0].table.size(0)
-        self.sel_table = torch.zeros(nqb, S, R, W, dtype=torch.int32, device=self.dev)
-        self.off_table = torch.zeros(nqb, S, R, 2, dtype=torch.int32, device=self.dev)
-        for i, s in enumerate(self.uniq_sched):
-            self.sel_table[:, i, :s.rows, :s.width] = s.table
-            self.off_table[:, i, :s.rows, 1] = s.counts
+        combos: dict = {}
+        combo_of = []
+        for p in range(self.max_len - self.start):
+            key = tuple(s.row_of[p] for s in self.uniq_sched)
+            combo_of.append(combos.setdefault(key, len(combos)))
+        self.combo_of = torch.tensor(combo_of, dtype=torch.long, device=self.dev)   # [positions]
+        self.sel_table = torch.zeros(len(combos), S, R, W, dtype=torch.int32, device=self.dev)
+        self.off_table = torch.zeros(len(combos), S, R, 2, dtype=torch.int32, device=self.dev)
+        for key, c in combos.items():
+            for i, (s, row) in enumerate(zip(self.uniq_sched, key)):
+                self.sel_table[c, i, :s.rows, :s.width] = s.table[row]
+                self.off_table[c, i, :s.rows, 1] = s.counts[row]
         self.sel_all = torch.zeros(1, S, R, W, dtype=torch.int32, device=self.dev)
         self.off_all = torch.zeros(1, S, R, 2, dtype=torch.int32, device=self.dev)
         for i, s in enumerate(self.uniq_sched):
             s.sel = self.sel_all[:, i, :s.rows, :s.width]
             s.sel_off = self.off_all[:, i, :s.rows, :]
 
-    def _select(self, qb_rel: torch.Tensor) -> None:
-        """Gathers the selections of query block ``qb0 + qb_rel`` (a device index) for every layer."""
-        torch.index_select(self.sel_table, 0, qb_rel, out=self.sel_all)
-        torch.index_select(self.off_table, 0, qb_rel, out=self.off_all)
+    def _select(self) -> None:
+        """Gathers every layer's selection for the current device position."""
+        combo = torch.index_select(self.combo_of, 0, self.pos - self.start)
+        torch.index_select(self.sel_table, 0, combo, out=self.sel_all)
+        torch.index_select(self.off_table, 0, combo, out=self.off_all)
 
     def _step(self) -> None:
         if self.fused:
@@ -272,10 +300,10 @@ class GraphDecoder:
         B, D, page = self.B, self.head_dim, self.page
         h = m.embed_tokens(self.ids[:, None])                                   # [B, 1, hidden]
         cos, sin = m.rotary_emb(h, self.pos.view(1, 1))
-        qb_rel = torch.div(self.pos, page, rounding_mode="floor") - self.qb0    # [1]
+        blk = torch.div(self.pos, page, rounding_mode="floor")                  # [1]
         slot = (self.pos % page).expand(B)                                      # [B]
         kv_len = (self.pos + 1).to(torch.int32).expand(B)
-        self._select(qb_rel)
+        self._select()
         for layer, store, sched in zip(self.layers, self.stores, self.sched):
             attn = layer.self_attn
             res = h
@@ -285,7 +313,7 @@ class GraphDecoder:
             k = attn.k_norm(attn.k_proj(x).view(shape)).transpose(1, 2)
             v = attn.v_proj(x).view(shape).transpose(1, 2)
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
-            pg = store.block_table.index_select(1, qb_rel + self.qb0).view(B).long()
+            pg = store.block_table.index_select(1, blk).view(B).long()
             store.k_pages[pg, :, slot] = k[:, :, 0].to(store.k_pages.dtype)
             store.v_pages[pg, :, slot] = v[:, :, 0].to(store.v_pages.dtype)
             store.kv_lens.copy_(kv_len)

@@ -11,8 +11,10 @@ produced: ``block_pairs``, ``block_pair_offsets``, ``kv_block_list``,
 mask.  These pin the functions that no published number or closed form pins:
 the rotation hash for heads other than 0 (``bigbird_pattern.py:23-41``), the
 per-group layout resolution of ``BigBirdKeepRatioPattern``
-(``bigbird_pattern.py:421-449``), ``BigBird2Pattern`` rows and the
-causal-block keep ratio (``bigbird_pattern.py:108-125``).
+(``bigbird_pattern.py:421-449``), ``BigBird2Pattern`` rows, the
+causal-block keep ratio (``bigbird_pattern.py:108-125``) and the
+``LocalWindowPattern`` schedule when queries sit after a cached prefix
+(``local_window.py:58-71``).
 
 Output: ``tests/golden/reference_patterns.npz`` (data only) and
 ``tests/golden/reference_patterns.json`` (the case list).
@@ -49,6 +51,12 @@ CASES = [
      {"group_sparsities": [0.5, 0.7, 0.8, 0.9], "n_kv_heads": 4}),
     ("bb2_t512_k128", "bigbird2", 512, 512, 4, {"top_k": 128}),
     ("bb2_dec_t700_k64", "bigbird2", 1, 700, 4, {"top_k": 64}),
+    # sliding window: square, decode (T_q = 1) and a chunk after a cached prefix (1 < T_q < T_k),
+    # where the query rows sit at max(0, T_k - T_q) + t (local_window.py:58-71)
+    ("lw_t300_w100_b32", "local", 300, 300, 2, {"window_size": 100, "block_size": 32}),
+    ("lw_dec_t777_w256_b64", "local", 1, 777, 2, {"window_size": 256, "block_size": 64}),
+    ("lw_chunk_q96_k300_w80_b16", "local", 96, 300, 2, {"window_size": 80, "block_size": 16}),
+    ("lw_chunk_q130_k1000_w512_b64", "local", 130, 1000, 3, {"window_size": 512, "block_size": 64}),
 ]
 
 MASK_LIMIT = 1 << 22   # store token masks up to 4M entries
@@ -57,7 +65,7 @@ MASK_LIMIT = 1 << 22   # store token masks up to 4M entries
 def main(ref_root: str) -> None:
     sys.path.insert(0, ref_root)
     from sparse_attentions.patterns import (  # noqa: E402  (reference, this container only)
-        BigBird2Pattern, BigBirdKeepRatioPattern, BigBirdPattern)
+        BigBird2Pattern, BigBirdKeepRatioPattern, BigBirdPattern, LocalWindowPattern)
 
     arrays: dict[str, np.ndarray] = {}
     index = []
@@ -66,6 +74,8 @@ def main(ref_root: str) -> None:
             pat = BigBirdPattern(top_k=params["top_k"], n_heads=H)
         elif kind == "bigbird2":
             pat = BigBird2Pattern(top_k=params["top_k"], n_heads=H)
+        elif kind == "local":
+            pat = LocalWindowPattern(window_size=params["window_size"], block_size=params["block_size"])
         else:
             kw = {k: v for k, v in params.items()}
             pat = BigBirdKeepRatioPattern(n_heads=H, **kw)
@@ -74,7 +84,8 @@ def main(ref_root: str) -> None:
         meta = pat.build(q, k, causal=True)
         arrays[f"{name}/block_pairs"] = meta.block_pairs.numpy().astype(np.int32)
         arrays[f"{name}/block_pair_offsets"] = meta.block_pair_offsets.numpy().astype(np.int32)
-        arrays[f"{name}/kv_block_list"] = meta.kv_block_list.numpy().astype(np.int32)
+        if meta.kv_block_list is not None:
+            arrays[f"{name}/kv_block_list"] = meta.kv_block_list.numpy().astype(np.int32)
         entry = {"name": name, "kind": kind, "T_q": T_q, "T_k": T_k, "n_heads": H,
                  "params": params, "block_size": int(meta.block_size),
                  "keep_ratio": float(meta.keep_ratio), "has_mask": False}

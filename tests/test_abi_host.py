@@ -64,9 +64,14 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     assert st == -2 and b"width >= 1" in lib.sa_last_error()
     st = lib.sa_block_mask_to_csr(None, 0, 0, 2, 4, 4, None, 0, None, None, 0, 0, None, None)
     assert st == -6
-    st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, None, 0, None, 0, 0, None, 0, 0,
+    st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, 0, None, 0, 0, None, 0, 0,
                        3, None, 0, 0, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
     assert st == -5 and b"sel_rows=3" in lib.sa_last_error()
+    # a paged table narrower than its own column count is refused before anything is read
+    fake = 16   # 16-byte aligned stand-in addresses; the call returns before any device access
+    st = lib.sa_decode(0, fake, 8, 8, fake, fake, 8, 8, 8, fake, 4, 8, 10, fake, 0, fake, 0, 0, fake, 0, 0,
+                       2, fake, 8, 8, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
+    assert st != 0 and b"block table of 8 columns" in lib.sa_last_error()
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 3) == 3 * 2 * 4 * 130 * 4
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 1) == 0
     assert lib.sa_prefill_workspace_bytes() == 8

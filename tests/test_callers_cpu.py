@@ -219,3 +219,31 @@ def test_group_sparsity_spec_precedence_and_parsing(tmp_path):
     merged.write_to(out)
     assert out.sparse_attention_group_sparsities == [0.1, 0.2]
     assert out.sparse_attention_layer_group_sparsities == [None, [0.7, 0.8]]
+
+
+@pytest.mark.parametrize("pattern", ["local100", "local512", "seeded"])
+def test_graph_decode_selection_per_position(pattern):
+    """The graph decoder's selection table gives every position exactly the schedule the eager
+    decode step builds at T_k = pos + 1, including a local window that moves inside a page."""
+    from sparseattentioninfer_amd.attention import HipBlockSparseBackend
+    from sparseattentioninfer_amd.patterns import LocalWindowPattern
+    from sparseattentioninfer_amd.qwen3.graph_decode import _LayerSchedule
+    pat = {"local100": LocalWindowPattern(window_size=100, block_size=64),
+           "local512": LocalWindowPattern(window_size=512, block_size=64),
+           "seeded": SeededBigBirdPattern(rows=2, block_size=64, window=3, global_blocks=2, random_blocks=3, seed=1)}[pattern]
+    attn = SimpleNamespace(num_heads=4, head_dim=128, num_key_value_heads=2, layer_idx=0,
+                           sparse_backend=HipBlockSparseBackend(), sparse_pattern=pat)
+    pos0, pos1 = 630, 780                       # crosses the page boundaries at 640 and 704
+    sch = _LayerSchedule(attn, SimpleNamespace(page=64), pos0, pos1, batch=1, device="cpu")
+    changes = 0
+    for pos in range(pos0, pos1):
+        meta = pat.build(torch.empty(1, 4, 1, 0), torch.empty(1, 2, pos + 1, 0))
+        pairs, offsets = meta.block_pairs, meta.block_pair_offsets
+        row = sch.row_of[pos - pos0]
+        for r in range(sch.rows):
+            want = pairs[r % pairs.size(0), offsets[r % pairs.size(0), 0]:offsets[r % pairs.size(0), 1]].tolist()
+            n = int(sch.counts[row, r])
+            assert sch.table[row, r, :n].tolist() == want, f"pos {pos} row {r}"
+        changes += pos > pos0 and sch.row_of[pos - pos0] != sch.row_of[pos - pos0 - 1]
+    # window 100 moves its first block inside pages (e.g. at pos 640 + 63 - 99 + ...); 512 and BigBird only at pages
+    assert changes >= 2

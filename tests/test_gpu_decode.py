@@ -86,9 +86,10 @@ def test_reference_bigbird_decode_through_backend():
     assert_close_bf16(out, want, "kr_groups_dec_t3000")
 
 
-def test_config4_full_size_sampled():
-    """B=64, 32Q/8KV, D=128, 16384 tokens in 64-token pages, 14 retained blocks per (seq, group)."""
-    _say("[decode] config 4 full size")
+def test_configs_3_full_size_every_sequence():
+    """B=64, 32Q/8KV, D=128, 16384 tokens in 64-token pages, 14 retained blocks per
+    (sequence, KV group), shuffled page table; every sequence and head checked."""
+    _say("[decode] configs[3] full size")
     B, Hq, Hkv, D, page, L = 64, 32, 8, 128, 64, 16384
     nblk = L // page
     P = B * nblk
@@ -99,11 +100,12 @@ def test_config4_full_size_sampled():
     table = torch.randperm(P, generator=torch.Generator().manual_seed(79)).to(torch.int32).reshape(B, nblk)
     kv_lens = torch.full((B,), L, dtype=torch.int32)
     sel, sel_off = decode_selection(B, Hkv, nblk, local=4, global_blocks=2, random_blocks=8, seed=80)
-    out = ops.paged_sparse_decode(q.to(DEV), kp, vp, table.to(DEV), kv_lens.to(DEV), sel.to(DEV), sel_off.to(DEV))
-    torch.cuda.synchronize()
-    pick = [0, 13, 63]
-    pages = table[pick].reshape(-1).long()
-    mini_table = torch.arange(len(pick) * nblk, dtype=torch.int32).reshape(len(pick), nblk)
-    want = oa.paged_decode_attention(q[pick], kp[pages.to(DEV)].cpu(), vp[pages.to(DEV)].cpu(), mini_table.numpy(),
-                                     kv_lens.numpy()[pick], sel.numpy()[pick], sel_off.numpy()[pick])
-    assert_close_bf16(out[pick], want, "config4 sampled")
+    assert (sel_off[:, :, 1] == 14).all()
+    for splits in (1, 2):
+        out = ops.paged_sparse_decode(q.to(DEV), kp, vp, table.to(DEV), kv_lens.to(DEV), sel.to(DEV),
+                                      sel_off.to(DEV), num_splits=splits)
+        torch.cuda.synchronize()
+        want = oa.paged_decode_attention(q, kp, vp, table.numpy(), kv_lens.numpy(), sel.numpy(), sel_off.numpy(),
+                                         device=DEV)
+        max_abs, mean_abs = assert_close_bf16(out, want, f"configs[3] splits={splits}")
+        _say(f"[decode] configs[3] splits={splits}: all 64 sequences, max-abs {max_abs:.3e}, mean-abs {mean_abs:.3e}")

@@ -130,3 +130,38 @@ def test_two_stage_argmax_equals_argmax():
               torch.randint(0, 4, (8, 151936), generator=g).float()):
         x = x.cuda()
         assert torch.equal(_argmax_rows(x, 128), x.argmax(-1))
+
+
+@torch.inference_mode()
+def test_graph_decode_local_window_moving_inside_a_page():
+    """A local window of 100 keys on 64-token pages moves its first block inside a page (positions
+    675, 739, ...): the graph must attend to exactly the blocks the eager step does at every position,
+    so teacher-forced logits track the eager ones across those positions and the page boundaries."""
+    _say("[graph] local window 100, 2 layers")
+    cfg = qwen3_config(num_hidden_layers=2, sparse_layers=[0], pattern="local", block_size=64,
+                       sparse_attention_window_size=100)
+    model = build_model(cfg, device="cuda", dtype=torch.bfloat16, seed=3)
+    assert model.model.layers[0].self_attn.sparse_pattern.window_size == 100
+    B, T, steps = 2, 630, 120                   # positions 630 .. 749
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(9)).cuda()
+    ce = PagedKVCache(cfg.num_hidden_layers, T + steps + 1, page=64, shuffle_seed=6)
+    nxt = model(input_ids=ids, past_key_values=ce, use_cache=True, logits_to_keep=1).logits[:, -1].argmax(-1)
+    inputs, eager = [], []
+    for _ in range(steps):
+        inputs.append(nxt.clone())
+        lg = model(input_ids=nxt[:, None], past_key_values=ce, use_cache=True, logits_to_keep=1).logits[:, -1]
+        nxt = lg.argmax(-1)
+        eager.append(lg.float().clone())
+    cg = PagedKVCache(cfg.num_hidden_layers, T + steps + 1, page=64, shuffle_seed=6)
+    first = model(input_ids=ids, past_key_values=cg, use_cache=True, logits_to_keep=1).logits[:, -1].argmax(-1)
+    dec = GraphDecoder(model, cg, first, T + steps, keep_logits=True, fused=True)
+    worst = 0.0
+    for s in range(steps):
+        dec.ids.copy_(inputs[s])
+        dec.step()
+        torch.cuda.synchronize()
+        diff = (dec.logits.float() - eager[s]).abs().max().item()
+        scale = eager[s].abs().max().item()
+        worst = max(worst, diff / max(1.0, scale))
+        assert diff <= 2e-2 * max(1.0, scale), f"step {s} (position {T + s}): logits max-abs diff {diff:.3e}"
+    _say(f"[graph] local window: {steps} teacher-forced steps, worst relative logit diff {worst:.2e}")

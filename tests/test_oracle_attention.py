@@ -145,3 +145,35 @@ def test_masked_sdpa_rows_equals_full_masked_sdpa():
     for h in range(H):
         rows = oa.masked_sdpa_rows(q[0, h, 5:17], k[0, h], v[0, h], (mask[h] & causal)[5:17])
         torch.testing.assert_close(rows, full[0, h, 5:17], atol=1e-12, rtol=0)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,T_q,T_k,bs,group_rows,chunk", [
+    (2, 4, 2, 80, 80, 16, True, 24),     # GQA, group rows, ragged tail, chunks not block-aligned
+    (1, 4, 4, 96, 96, 32, False, 1000),  # one chunk
+    (1, 2, 1, 40, 100, 16, True, 16),    # chunked prefill: T_q < T_k, q_offset = 60
+])
+def test_masked_sdpa_blockwise_equals_masked_sdpa(B, Hq, Hkv, T_q, T_k, bs, group_rows, chunk):
+    """The row-chunked block-mask form used for exhaustive checks at 32K tokens equals
+    masked_sdpa on the expanded token mask (and so, transitively, the float64 textbook loop)."""
+    D = 8
+    q, k, v = _rand((B, Hq, T_q, D), 61), _rand((B, Hkv, T_k, D), 62), _rand((B, Hkv, T_k, D), 63)
+    R = Hkv if group_rows else Hq
+    nqb, nkb = -(-T_q // bs), -(-T_k // bs)
+    bm = torch.from_numpy(np.random.default_rng(T_q).random((R, nqb, nkb)) < 0.45)
+    got = oa.masked_sdpa_blockwise(q, k, v, bm, bs, row_chunk=chunk)
+    rowmap = np.arange(Hq) // (Hq // R)
+    tok = bm.repeat_interleave(bs, 1).repeat_interleave(bs, 2)[:, :T_q, :T_k][rowmap]
+    off = T_k - T_q
+    causal = torch.arange(T_k)[None, :] <= (off + torch.arange(T_q))[:, None]
+    n_rep = Hq // Hkv
+    if T_q == T_k:
+        want = oa.masked_sdpa(q, oa.repeat_kv(k, n_rep), oa.repeat_kv(v, n_rep), "mask", tok)
+    else:   # masked_sdpa cannot broadcast its causal mask for 1 < T_q < T_k: textbook loop per head
+        want = torch.stack([torch.from_numpy(oa.textbook_attention(
+            q[b, h], k[b, h // n_rep], v[b, h // n_rep], (tok[h] & causal).numpy())).float()
+            for b in range(B) for h in range(Hq)]).reshape(B, Hq, T_q, D)
+    torch.testing.assert_close(got, want.float(), atol=2e-6, rtol=0)
+    # and it matches the block-gather oracle over the same schedule
+    pairs, offsets = ocsr.csr_from_block_mask(bm.numpy())
+    gather = oa.block_sparse_attention(q, k, v, pairs, offsets, bs)
+    torch.testing.assert_close(got, gather, atol=2e-6, rtol=0)

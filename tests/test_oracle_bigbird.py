@@ -50,7 +50,8 @@ def test_planted_hash_mistake_breaks_published_ratio(monkeypatch):
 
 
 def _golden():
-    idx = json.loads((GOLDEN / "reference_patterns.json").read_text())
+    """The BigBird-family golden cases (the local-window ones are pinned with the pattern classes)."""
+    idx = [c for c in json.loads((GOLDEN / "reference_patterns.json").read_text()) if c["kind"] != "local"]
     data = np.load(GOLDEN / "reference_patterns.npz")
     return idx, data
 

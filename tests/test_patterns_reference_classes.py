@@ -31,6 +31,8 @@ def _pattern(case):
         return BigBirdPattern(top_k=p["top_k"], n_heads=case["n_heads"])
     if case["kind"] == "bigbird2":
         return BigBird2Pattern(top_k=p["top_k"], n_heads=case["n_heads"])
+    if case["kind"] == "local":
+        return LocalWindowPattern(window_size=p["window_size"], block_size=p["block_size"])
     if "group_sparsities" in p:
         return BigBirdKeepRatioPattern(group_sparsities=p["group_sparsities"], n_heads=case["n_heads"],
                                        n_kv_heads=p.get("n_kv_heads"))
@@ -42,11 +44,16 @@ def test_pattern_classes_match_reference_outputs(name):
     case, d = golden_case(name)
     pat = _pattern(case)
     meta = pat.build(*_qk(case["T_q"], case["T_k"], case["n_heads"]))
-    assert meta.kind == "mask" and meta.block_size == case["block_size"]
+    assert meta.kind == ("local" if case["kind"] == "local" else "mask")
+    assert meta.block_size == case["block_size"]
     assert np.array_equal(meta.block_pairs.numpy(), d["block_pairs"])
     assert np.array_equal(meta.block_pair_offsets.numpy(), d["block_pair_offsets"])
-    assert np.array_equal(meta.kv_block_list.numpy(), d["kv_block_list"])
-    assert meta.block_pairs.dtype == torch.int32 and meta.kv_block_list.dtype == torch.int32
+    assert meta.block_pairs.dtype == torch.int32
+    if "kv_block_list" in d:
+        assert np.array_equal(meta.kv_block_list.numpy(), d["kv_block_list"])
+        assert meta.kv_block_list.dtype == torch.int32
+    else:
+        assert meta.kv_block_list is None
     assert meta.keep_ratio == pytest.approx(case["keep_ratio"], abs=0, rel=1e-15)
     if "mask" in d:
         assert np.array_equal(meta.mask.numpy(), d["mask"])
@@ -124,3 +131,16 @@ def test_mask_is_lazy_and_cached():
     first = m1.mask
     m2 = pat.build(*_qk(512, 512, 2))
     assert m2.mask is first                   # built once per shape
+
+
+@pytest.mark.parametrize("name", [c for c in CASES if c.startswith("lw_")])
+def test_oracle_local_window_matches_reference_outputs(name):
+    """The oracle's restatement against the reference's own LocalWindowPattern, including
+    queries after a cached prefix (T_q < T_k: rows at max(0, T_k - T_q) + t)."""
+    case, d = golden_case(name)
+    T_q, T_k, H, p = case["T_q"], case["T_k"], case["n_heads"], case["params"]
+    mask = ob.local_window_token_mask(T_q, T_k, H, p["window_size"])
+    assert np.array_equal(mask, d["mask"])
+    pairs, offsets = ob.local_window_schedule(T_q, T_k, H, p["window_size"], p["block_size"])
+    assert np.array_equal(pairs, d["block_pairs"]) and np.array_equal(offsets, d["block_pair_offsets"])
+    assert ob.local_window_keep_ratio(T_q, T_k, p["window_size"]) == pytest.approx(case["keep_ratio"], rel=1e-15)
