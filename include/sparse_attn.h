@@ -194,6 +194,34 @@ int sa_decode(int dtype,
 int64_t sa_decode_workspace_bytes(int B, int Hq, int D, int num_splits);
 
 /*
+ * sa_decode without a workspace argument: no counterpart in the reference.  For
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  The split partials
+ * (num_splits > 1) live in a file-scope device array of
+ * sa_decode_noalloc_scratch_bytes() = 16 MiB that each GPU holds until the
+ * process ends; sizes needing more are refused with SA_E_WORKSPACE.  It calls
+ * no hipMalloc, hipFree or allocating routine (the array's device address is
+ * looked up once per device on the first call).  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU (other streams, other
+ * threads) race, so serialise them.  Same results, bit for bit, as sa_decode.
+ */
+int sa_decode_noalloc(int dtype,
+                      const void* q, int64_t q_sb, int64_t q_sh,
+                      const void* k, const void* v,
+                      int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+                      const int32_t* block_table, int64_t bt_stride, int max_blocks, int num_pages,
+                      const int32_t* kv_lens, int kv_len,
+                      const int32_t* sel, int64_t sel_sb, int64_t sel_sr,
+                      const int32_t* sel_off, int64_t off_sb, int64_t off_sr,
+                      int sel_rows,
+                      void* o, int64_t o_sb, int64_t o_sh,
+                      int B, int Hq, int Hkv, int D, int page, float sm_scale,
+                      int num_splits, void* stream);
+
+/* Bytes of the scratch array sa_decode_noalloc holds per GPU. */
+int64_t sa_decode_noalloc_scratch_bytes(void);
+
+/*
  * Fused elementwise stages of one decode step of a Qwen3 decoder layer, for the
  * graph-captured end-to-end decode (callers of the attention path, not the
  * attention itself).  They keep Hugging Face's arithmetic: fp32 inside,

@@ -72,6 +72,21 @@ SIGNATURES = {
         _vp,
     ]),
     "sa_decode_workspace_bytes": (_i64, [_i32, _i32, _i32, _i32]),
+    "sa_decode_noalloc": (_i32, [
+        _i32,
+        _vp, _i64, _i64,
+        _vp, _vp,
+        _i64, _i64, _i64,
+        _vp, _i64, _i32, _i32,
+        _vp, _i32,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
+        _i32,
+        _vp, _i64, _i64,
+        _i32, _i32, _i32, _i32, _i32, _f32,
+        _i32, _vp,
+    ]),
+    "sa_decode_noalloc_scratch_bytes": (_i64, []),
     "sa_rmsnorm": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "sa_qk_rope_kv": (_i32, [
         _i32, _vp, _i64, _vp, _vp, _vp, _vp,

@@ -15,6 +15,8 @@
 //  * q.k partial dots are reduced across the D/8 lanes of a row with xor-shuffles;
 //    the online softmax keeps (m, l, acc) per head; waves merge through LDS, and
 //    splits (num_splits > 1) merge in decode_combine_kernel.
+#include <mutex>
+
 #include "sa_common.h"
 
 namespace sa {
@@ -481,4 +483,73 @@ extern "C" int sa_decode(int dtype,
   }
   if (err != hipSuccess) return set_error((int)err, "sa_decode: launch failed: %s", hipGetErrorString(err));
   return 0;
+}
+
+// ---- no-allocation entry point ------------------------------------------------------------
+// sa_decode with its split partials in a file-scope device array instead of a caller workspace,
+// for callers that cannot allocate device memory.  Each GPU holds its own copy of the array; its
+// device address comes from hipGetSymbolAddress once per device (the array's name in host code
+// is not a device address) and is kept in noalloc_ptr.
+namespace sa {
+
+constexpr int64_t NOALLOC_SCRATCH_BYTES = (int64_t)16 << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+static std::mutex noalloc_mu;
+static void* noalloc_ptr[NOALLOC_MAX_DEVICES] = {nullptr};
+
+// Device address of the current device's scratch array (set up on the first call per device).
+static int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error((int)e, "sa_decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+    return set_error(SA_E_SHAPE, "sa_decode_noalloc: device %d past the %d supported", dev, NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(noalloc_mu);
+  if (!noalloc_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(e != hipSuccess ? (int)e : SA_E_NULL, "sa_decode_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                       hipGetErrorString(e));
+    noalloc_ptr[dev] = p;
+  }
+  *out = noalloc_ptr[dev];
+  return 0;
+}
+
+}  // namespace sa
+
+extern "C" int64_t sa_decode_noalloc_scratch_bytes(void) { return sa::NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int sa_decode_noalloc(int dtype,
+                                 const void* q, int64_t q_sb, int64_t q_sh,
+                                 const void* k, const void* v,
+                                 int64_t kv_sb, int64_t kv_sh, int64_t kv_st,
+                                 const int32_t* block_table, int64_t bt_stride, int max_blocks, int num_pages,
+                                 const int32_t* kv_lens, int kv_len,
+                                 const int32_t* sel, int64_t sel_sb, int64_t sel_sr,
+                                 const int32_t* sel_off, int64_t off_sb, int64_t off_sr,
+                                 int sel_rows,
+                                 void* o, int64_t o_sb, int64_t o_sh,
+                                 int B, int Hq, int Hkv, int D, int page, float sm_scale,
+                                 int num_splits, void* stream) {
+  using namespace sa;
+  clear_error();
+  const int64_t need = sa_decode_workspace_bytes(B, Hq, D, num_splits);
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return set_error(SA_E_WORKSPACE,
+                     "sa_decode_noalloc: B=%d Hq=%d D=%d num_splits=%d needs %lld scratch bytes, more than the %lld "
+                     "held (use sa_decode with a workspace, or fewer splits)",
+                     B, Hq, D, num_splits, (long long)need, (long long)NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc) return rc;
+  }
+  return sa_decode(dtype, q, q_sb, q_sh, k, v, kv_sb, kv_sh, kv_st, block_table, bt_stride, max_blocks, num_pages,
+                   kv_lens, kv_len, sel, sel_sb, sel_sr, sel_off, off_sb, off_sr, sel_rows, o, o_sb, o_sh, B, Hq,
+                   Hkv, D, page, sm_scale, num_splits, ws, need, stream);
 }
