@@ -173,6 +173,45 @@ def run_prefill_bernoulli(args, dev):
                          "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None}}
 
 
+def run_pattern_build(dev, reps: int = 20):
+    """Schedule construction time (block mask + CSR), the cost the reference pays in Python per
+    shape (11.61 ms for BigBird top_k=64 at T=2048, ``bigbird_triton_vs_masked.csv`` row 63).
+    Each build is a fresh pattern object (no cache), timed to its last GPU operation."""
+    import torch
+    from sparseattentioninfer_amd.patterns import BigBirdPattern, SeededBigBirdPattern
+
+    def timed(make, q, k, n):
+        make().build(q, k)                                    # warm (kernels, allocator)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            make().build(q, k)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / n * 1e3
+
+    T, Hq, Hkv = 32768, 32, 8
+    q = torch.empty(1, Hq, T, 0, device=dev)
+    k = torch.empty(1, Hkv, T, 0, device=dev)
+    counts = [0, 1, 2, 3, 3, 4, 6, 8]
+    seeded = lambda rng: (lambda: SeededBigBirdPattern(rows=Hkv, window=3, global_blocks=2, random_blocks=counts,  # noqa: E731
+                                                       seed=7, rng=rng))
+    gpu_ms = timed(seeded("philox"), q, k, reps)
+    cpu_ms = timed(seeded("torch"), q, k, 2)
+    q2 = torch.empty(1, 8, 2048, 0, device=dev)
+    ref_ms = timed(lambda: BigBirdPattern(top_k=64, n_heads=8), q2, q2, reps)
+    big_ms = timed(lambda: BigBirdPattern(top_k=256, n_heads=Hq), torch.empty(1, Hq, T, 0, device=dev),
+                   torch.empty(1, Hq, T, 0, device=dev), reps)
+    return {"configs2_seeded_bigbird_gpu_ms": gpu_ms,
+            "configs2_seeded_bigbird_cpu_torch_ms": cpu_ms,
+            "reference_bigbird_t2048_topk64_h8_gpu_ms": ref_ms,
+            "reference_bigbird_t2048_topk64_published_python_ms": 11.61,
+            "reference_bigbird_t32768_topk256_h32_gpu_ms": big_ms,
+            "note": ("block mask + CSR per shape, fresh pattern object per build (no cache), host-timed to the "
+                     "last GPU operation; gpu = HIP generators + HIP CSR (one host read of the CSR width); "
+                     "cpu_torch = the CPU generator + torch packing + copy to the GPU; the published figure is "
+                     "the reference's Python build on its own (unstated) hardware")}
+
+
 def decode_workload(dev):
     """paged bf16 cache, 64 sequences x 16384 tokens, BigBird-style block selection."""
     import torch
@@ -392,6 +431,9 @@ def main():
         if pre is None:
             line.update(value=round(dec["tok_per_s"], 1), unit="tok/s", ms_per_step=round(dec["us_per_step"] / 1e3, 4),
                         config={"workload": dec["workload"]}, roofline=line["decode"]["roofline"])
+    if args.only == "all":
+        pb = run_pattern_build(dev)
+        line["pattern_build"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pb.items()}
     if not args.no_e2e and args.only == "all":
         try:
             e2e = run_e2e(args, dev)

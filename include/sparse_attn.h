@@ -130,16 +130,55 @@ int64_t sa_prefill_workspace_bytes(void);
  * mask_qb_stride, key blocks contiguous.  Writes offsets [rows, nqb + 1]
  * (row stride offsets_stride) and nnz [rows] (retained blocks per row).  With
  * pairs == NULL this is the count pass; with pairs [rows, width] (row stride
- * pairs_stride) it also writes the ascending key blocks of every query block
- * and zero-pads each row to width.  The reference's width is
- * max(1, max nnz), known after the count pass.  *status (a device int the
- * caller zeroes) receives 1 if a row holds more than width blocks.
+ * pairs_stride) it is the write pass: it reads the offsets the count pass
+ * wrote, writes the ascending key blocks of every query block and zero-pads
+ * each row to width.  The reference's width is max(1, max nnz), known after
+ * the count pass.  *status (a device int the caller zeroes) receives 1 if a
+ * row holds more than width blocks.  Each mask row is read by one wave with
+ * consecutive lanes on consecutive bytes.
  */
 int sa_block_mask_to_csr(const uint8_t* mask, int64_t mask_row_stride, int64_t mask_qb_stride,
                          int rows, int nqb, int nkb,
                          int32_t* offsets, int64_t offsets_stride, int32_t* nnz,
                          int32_t* pairs, int64_t pairs_stride, int64_t width,
                          int* status, void* stream);
+
+/*
+ * Block-mask generators (byte masks as sa_block_mask_to_csr reads them, 1 =
+ * retained).  mask [rows, nqb, mask_qb_stride] with mask_qb_stride and
+ * mask_row_stride multiples of 16 and at least nkb (resp. nqb *
+ * mask_qb_stride); bytes past nkb are written 0.  Query block i sits at
+ * absolute block q_block_offset + i.  No host round trip, nothing
+ * synchronised.
+ *
+ * sa_bigbird_block_mask: the reference's BigBird rows (bigbird_pattern.py:23-41
+ * random pick, :246-255 row sets) with layout[3*row .. 3*row+2] = (global,
+ * sliding, random) per row (device int32), hash head head_base + row,
+ * num_blocks hash_blocks in the hash; dense_last_block != 0 keeps every block
+ * of the last query block (BigBird2Pattern).  Replaces the per-row Python loops
+ * of BigBirdPattern._get_block_pairs / BigBirdKeepRatioPattern
+ * (bigbird_pattern.py:212-335, :533-634).
+ *
+ * sa_seeded_bigbird_block_mask / sa_bernoulli_block_mask: this build's seeded
+ * benchmark generators (no counterpart in the reference, whose "random" blocks
+ * are a hash) on Philox4x64-10: the draw of block kb of query block qa (causal
+ * limit min(q_block_offset + i, nkb - 1)) in row `row` is the first word of
+ * philox(counter = (kb, qa, row, 0), key = (seed, 1 for BigBird, 2 for
+ * Bernoulli)).  Bernoulli keeps kb < qa iff (draw >> 11) < floor(density *
+ * 2^53), and the diagonal.  Seeded BigBird keeps the global prefix, the window
+ * (trailing {qa-window+1..qa}, or centred {qa-window/2..qa+window/2} when
+ * centred != 0) and the diagonal, causal-truncated, plus the
+ * random_counts[row] (device int32) eligible blocks with the smallest
+ * (draw, kb).
+ */
+int sa_bigbird_block_mask(uint8_t* mask, int64_t mask_row_stride, int64_t mask_qb_stride, int rows, int nqb,
+                          int nkb, int q_block_offset, const int32_t* layout, int head_base, int hash_blocks,
+                          int dense_last_block, void* stream);
+int sa_seeded_bigbird_block_mask(uint8_t* mask, int64_t mask_row_stride, int64_t mask_qb_stride, int rows,
+                                 int nqb, int nkb, int q_block_offset, int window, int global_blocks, int centred,
+                                 const int32_t* random_counts, uint64_t seed, void* stream);
+int sa_bernoulli_block_mask(uint8_t* mask, int64_t mask_row_stride, int64_t mask_qb_stride, int rows, int nqb,
+                            int nkb, int q_block_offset, double density, uint64_t seed, void* stream);
 
 int sa_csr_to_tiles(const int32_t* pairs, int64_t pairs_stride,
                     const int32_t* offsets, int64_t offsets_stride,

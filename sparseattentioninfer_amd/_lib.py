@@ -19,10 +19,15 @@ _LIB = None
 _LOCK = threading.Lock()
 
 _i32, _i64, _f32, _vp = ctypes.c_int, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+_u64, _f64 = ctypes.c_uint64, ctypes.c_double
 
 # Exported entry points and their argument types (mirrors include/sparse_attn.h).
 SIGNATURES = {
     "sa_abi_version": (_i32, []),
+    "sa_bigbird_block_mask": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _i32, _vp, _i32, _i32, _i32, _vp]),
+    "sa_seeded_bigbird_block_mask": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _u64,
+                                            _vp]),
+    "sa_bernoulli_block_mask": (_i32, [_vp, _i64, _i64, _i32, _i32, _i32, _i32, _f64, _u64, _vp]),
     "sa_last_error": (ctypes.c_char_p, []),
     "sa_prefill": (_i32, [
         _i32,

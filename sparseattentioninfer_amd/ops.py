@@ -123,6 +123,65 @@ def block_mask_to_csr_gpu(block_active: torch.Tensor) -> tuple[torch.Tensor, tor
     return pairs, offsets
 
 
+def _mask_buffer(rows: int, nqb: int, nkb: int, device) -> torch.Tensor:
+    """Byte mask ``[rows, nqb, nkb]`` as the generators write it: a view of a buffer whose
+    query-block stride is NKB rounded up to 16 bytes."""
+    sq = -(-max(1, nkb) // 16) * 16
+    return torch.empty(rows, nqb, sq, dtype=torch.uint8, device=device)[:, :, :nkb]
+
+
+def _mask_call(name: str, fn, buf: torch.Tensor, rows: int, nqb: int, nkb: int, *args) -> torch.Tensor:
+    _lib.check(name, fn(buf.data_ptr(), buf.stride(0), buf.stride(1), rows, nqb, nkb, *args))
+    return buf
+
+
+def bigbird_block_mask_gpu(nqb: int, nkb: int, q_block_offset: int, layout: torch.Tensor, *,
+                           head_base: int = 0, hash_blocks: int | None = None, dense_last: bool = False,
+                           device=None) -> torch.Tensor:
+    """The reference's BigBird rows as a ``[R, NQB, NKB]`` uint8 mask built on the GPU.
+
+    ``layout [R, 3]`` int (global, sliding, random) per row; row ``r`` hashes as head
+    ``head_base + r`` with ``hash_blocks`` (default NKB) blocks (``bigbird_pattern.py:23-41``).
+    """
+    device = torch.device(device) if device is not None else layout.device
+    _require(device.type == "cuda", "bigbird_block_mask_gpu: needs a GPU device")
+    lay = layout.to(device=device, dtype=torch.int32).contiguous()
+    _require(lay.dim() == 2 and lay.size(1) == 3, "bigbird_block_mask_gpu: layout must be [R, 3]")
+    R = lay.size(0)
+    buf = _mask_buffer(R, nqb, nkb, device)
+    hb = nkb if hash_blocks is None else int(hash_blocks)
+    return _mask_call("sa_bigbird_block_mask", _lib.load().sa_bigbird_block_mask, buf, R, nqb, nkb,
+                      int(q_block_offset), lay.data_ptr(), int(head_base), hb, int(bool(dense_last)),
+                      torch.cuda.current_stream(device).cuda_stream)
+
+
+def seeded_bigbird_block_mask_gpu(rows: int, nqb: int, nkb: int, *, window: int, global_blocks: int,
+                                  random_blocks, seed: int, window_align: str = "trailing",
+                                  q_block_offset: int = 0, device="cuda") -> torch.Tensor:
+    """Seeded BigBird rows on Philox4x64-10 (see ``include/sparse_attn.h``), ``[R, NQB, NKB]`` uint8."""
+    _require(window_align in ("trailing", "centred"), f"window_align must be 'trailing' or 'centred', got {window_align!r}")
+    device = torch.device(device)
+    counts = torch.as_tensor(random_blocks, dtype=torch.int32).reshape(-1)
+    if counts.numel() == 1:
+        counts = counts.expand(rows)
+    _require(counts.numel() == rows, f"random_blocks has {counts.numel()} entries for {rows} rows")
+    counts = counts.contiguous().to(device)
+    buf = _mask_buffer(rows, nqb, nkb, device)
+    return _mask_call("sa_seeded_bigbird_block_mask", _lib.load().sa_seeded_bigbird_block_mask, buf, rows, nqb,
+                      nkb, int(q_block_offset), int(window), int(global_blocks), int(window_align == "centred"),
+                      counts.data_ptr(), int(seed) & ((1 << 64) - 1), torch.cuda.current_stream(device).cuda_stream)
+
+
+def bernoulli_block_mask_gpu(rows: int, nqb: int, nkb: int, *, density: float, seed: int, q_block_offset: int = 0,
+                             device="cuda") -> torch.Tensor:
+    """Bernoulli(density) rows on Philox4x64-10, diagonal kept, ``[R, NQB, NKB]`` uint8."""
+    device = torch.device(device)
+    buf = _mask_buffer(rows, nqb, nkb, device)
+    return _mask_call("sa_bernoulli_block_mask", _lib.load().sa_bernoulli_block_mask, buf, rows, nqb, nkb,
+                      int(q_block_offset), float(density), int(seed) & ((1 << 64) - 1),
+                      torch.cuda.current_stream(device).cuda_stream)
+
+
 def _schedule_args(pairs, offsets, block_size, tiles: TileSchedule | None):
     """Schedule arguments of sa_prefill: (pairs, offsets, masks) tensors to keep alive, the six
     pointer/stride arguments, and the number of schedule query blocks."""

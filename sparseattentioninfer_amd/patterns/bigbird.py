@@ -123,9 +123,31 @@ def bigbird_block_rows(qb_abs: torch.Tensor, heads: torch.Tensor, num_blocks: in
     return keep
 
 
+def bigbird_block_mask(q_block_offset: int, nqb: int, num_blocks: int, g: torch.Tensor, s: torch.Tensor,
+                       r: torch.Tensor, device, dense_last: bool = False) -> torch.Tensor:
+    """Retained key blocks of rows ``0 .. R-1`` (hash head = row) for query blocks
+    ``q_block_offset + i``: on a GPU from the HIP generator (``sa_bigbird_block_mask``, one
+    launch), elsewhere with :func:`bigbird_block_rows`.  ``dense_last`` keeps every block of
+    the last query block (BigBird2).  Returns ``[R, NQB, num_blocks]`` (uint8 on the GPU, bool
+    elsewhere; the CSR builders take either)."""
+    device = torch.device(device)
+    if device.type == "cuda":
+        from .. import ops
+        layout = torch.stack([g.reshape(-1), s.reshape(-1), r.reshape(-1)], dim=1)
+        return ops.bigbird_block_mask_gpu(nqb, num_blocks, q_block_offset, layout, dense_last=dense_last,
+                                          device=device)
+    R = g.numel()
+    bm = bigbird_block_rows(q_block_offset + torch.arange(nqb, device=device), torch.arange(R, device=device),
+                            num_blocks, g, s, r)
+    if dense_last and nqb:
+        bm[:, -1, :] = True
+    return bm
+
+
 def _padded_list(block_mask: torch.Tensor, max_kv: int) -> torch.Tensor:
     """``[R, NQB, NKB]`` bool -> ``[R, NQB, max_kv]`` int32 ascending ids, first max_kv, -1 padded."""
     R, nqb, nkb = block_mask.shape
+    block_mask = block_mask.bool()
     out = torch.full((R, nqb, max_kv), -1, dtype=torch.int32, device=block_mask.device)
     rank = torch.cumsum(block_mask.to(torch.int32), dim=2) - 1          # slot of each kept block
     sel = block_mask & (rank < max_kv)
@@ -163,6 +185,8 @@ def _cached_mask(entry: dict, build: Callable[[], torch.Tensor]) -> Callable[[],
 class BigBirdPattern(SparsePattern):
     """Global + sliding-window + random blocks from a top-k budget (``bigbird_pattern.py:130-335``)."""
 
+    _dense_last = False   # BigBird2: the last query block keeps every key block
+
     def __init__(self, top_k: int, n_heads: int):
         self.top_k = top_k
         self.n_heads = n_heads
@@ -178,10 +202,9 @@ class BigBirdPattern(SparsePattern):
         nqb, nkb = -(-T_q // tbs), -(-T_k // tbs)
         qbo = max(0, T_k - T_q) // tbs
         H = self.n_heads
-        heads = torch.arange(H, device=device)
         full = lambda v: torch.full((H,), v, device=device)
-        bm = bigbird_block_rows(qbo + torch.arange(nqb, device=device), heads, nkb, full(g), full(s), full(r))
-        return bm, tbs, max(1, g + s + r)
+        bm = bigbird_block_mask(qbo, nqb, nkb, full(g), full(s), full(r), device, dense_last=self._dense_last)
+        return bm, tbs, max(1, g + s + r) if not self._dense_last else max(nkb, g + s + r)
 
     def _mask_fn(self, T_q: int, T_k: int, device: torch.device) -> Callable[[], torch.Tensor]:
         def build():   # ``_get_mask``, ``bigbird_pattern.py:173-210``: absolute query blocks
@@ -214,10 +237,7 @@ class BigBirdPattern(SparsePattern):
 class BigBird2Pattern(BigBirdPattern):
     """BigBird whose last query block attends to every key block (``bigbird_pattern.py:636-806``)."""
 
-    def _schedule_rows(self, T_q: int, T_k: int, device: torch.device):
-        bm, tbs, max_kv = super()._schedule_rows(T_q, T_k, device)
-        bm[:, -1, :] = True
-        return bm, tbs, max(bm.shape[2], max_kv)
+    _dense_last = True
 
     def _mask_fn(self, T_q: int, T_k: int, device: torch.device) -> Callable[[], torch.Tensor]:
         def build():   # ``_get_mask``, ``bigbird_pattern.py:648-695``: local query blocks
@@ -303,8 +323,7 @@ class BigBirdKeepRatioPattern(SparsePattern):
             tbs = next_pow2_min16(layouts[0][0])
             nqb, nkb = -(-T_q // tbs), -(-T_k // tbs)
             g, s, r = self._head_params(layouts, device)
-            qa = max(0, T_k - T_q) // tbs + torch.arange(nqb, device=device)
-            bm = bigbird_block_rows(qa, torch.arange(self.n_heads, device=device), nkb, g, s, r)
+            bm = bigbird_block_mask(max(0, T_k - T_q) // tbs, nqb, nkb, g, s, r, device)
             pairs, offsets = block_mask_to_csr(bm)
             kv = _padded_list(bm, max(1, max(lg + ls + lr for _, lg, ls, lr in layouts)))
             self._cache[key] = {"pairs": pairs, "offsets": offsets, "kv": kv, "bs": tbs,

@@ -3,10 +3,14 @@
 The reference's BigBird "random" blocks are a deterministic hash
 (``sparse_attentions/patterns/bigbird_pattern.py:23-41``); the workloads this
 build is measured on instead draw random blocks from a seeded generator, and
-use per-KV-group masks shared by the query heads of a group.  Everything is
-generated at block level ``[R, NQB, NKB]`` on the CPU with a
-``torch.Generator`` (reproducible across machines), then turned into the
-reference's CSR format by :func:`block_mask_to_csr`.
+use per-KV-group masks shared by the query heads of a group.  Masks are
+generated at block level ``[R, NQB, NKB]``, then turned into the reference's
+CSR format by :func:`block_mask_to_csr`: by default on the CPU with a
+``torch.Generator`` (reproducible across machines; the committed benchmark
+workloads use it), or with ``rng="philox"`` on the query's GPU by the HIP
+generators (``ops.seeded_bigbird_block_mask_gpu`` / ``bernoulli_block_mask_gpu``,
+Philox4x64-10), with the CSR built there too -- no host round trip but the
+one read of the CSR width.
 
 Rows here are CSR rows: one per KV group when the pattern is group-shared.
 """
@@ -98,13 +102,26 @@ class _BlockMaskPattern(SparsePattern):
 
     CACHE_SIZE = 32
 
-    def __init__(self, block_size: int, rows: int):
+    def __init__(self, block_size: int, rows: int, rng: str = "torch"):
+        if rng not in ("torch", "philox"):
+            raise ValueError(f"rng must be 'torch' (CPU generator) or 'philox' (GPU generator), got {rng!r}")
         self.block_size = int(block_size)
         self.rows = int(rows)
+        self.rng = rng
         self._cache: OrderedDict = OrderedDict()
 
-    def _block_mask(self, nqb: int, nkb: int, q_block_offset: int) -> torch.Tensor:
+    def _block_mask(self, nqb: int, nkb: int, q_block_offset: int, device) -> torch.Tensor:
         raise NotImplementedError
+
+    def _device_for(self, device: torch.device):
+        """Where the block mask is generated: the CPU generator's masks on the CPU, the Philox
+        generator's on the query's GPU (it has no CPU implementation in the product)."""
+        if self.rng == "torch":
+            return torch.device("cpu")
+        if device.type != "cuda":
+            raise RuntimeError("rng='philox' generates block masks on the GPU; the query is on "
+                               f"{device.type}")
+        return device
 
     def build(self, q: torch.Tensor, k: torch.Tensor, causal: bool = True) -> PatternMetadata:
         T_q, T_k = q.size(2), k.size(2)
@@ -113,7 +130,7 @@ class _BlockMaskPattern(SparsePattern):
         key = (nqb, nkb, qbo, str(q.device))
         entry = self._cache.get(key)
         if entry is None:
-            pairs, offsets = block_mask_to_csr(self._block_mask(nqb, nkb, qbo))
+            pairs, offsets = block_mask_to_csr(self._block_mask(nqb, nkb, qbo, self._device_for(q.device)))
             kept = int(offsets[:, -1].long().sum())
             entry = (pairs.to(q.device), offsets.to(q.device), kept)
             self._cache[key] = entry
@@ -132,12 +149,19 @@ class SeededBigBirdPattern(_BlockMaskPattern):
     """BigBird with seeded random blocks; ``rows`` CSR rows (Hq, or Hkv for group sharing)."""
 
     def __init__(self, *, rows: int, block_size: int = 64, window: int = 3, global_blocks: int = 2,
-                 random_blocks=3, seed: int = 0, window_align: str = "trailing"):
-        super().__init__(block_size, rows)
+                 random_blocks=3, seed: int = 0, window_align: str = "trailing", rng: str = "torch"):
+        super().__init__(block_size, rows, rng)
         self.window, self.global_blocks = window, global_blocks
         self.random_blocks, self.seed, self.window_align = random_blocks, seed, window_align
 
-    def _block_mask(self, nqb, nkb, qbo):
+    def _block_mask(self, nqb, nkb, qbo, device):
+        if self.rng == "philox":
+            from .. import ops
+            return ops.seeded_bigbird_block_mask_gpu(self.rows, nqb, nkb, window=self.window,
+                                                     global_blocks=self.global_blocks,
+                                                     random_blocks=self.random_blocks, seed=self.seed,
+                                                     window_align=self.window_align, q_block_offset=qbo,
+                                                     device=device)
         return seeded_bigbird_block_mask(self.rows, nqb, nkb, window=self.window,
                                          global_blocks=self.global_blocks,
                                          random_blocks=self.random_blocks, seed=self.seed,
@@ -147,11 +171,15 @@ class SeededBigBirdPattern(_BlockMaskPattern):
 class BernoulliBlockPattern(_BlockMaskPattern):
     """Arbitrary-pattern workload: Bernoulli(density) blocks per CSR row, diagonal kept."""
 
-    def __init__(self, *, rows: int, density: float, block_size: int = 64, seed: int = 0):
-        super().__init__(block_size, rows)
+    def __init__(self, *, rows: int, density: float, block_size: int = 64, seed: int = 0, rng: str = "torch"):
+        super().__init__(block_size, rows, rng)
         self.density, self.seed = density, seed
 
-    def _block_mask(self, nqb, nkb, qbo):
+    def _block_mask(self, nqb, nkb, qbo, device):
+        if self.rng == "philox":
+            from .. import ops
+            return ops.bernoulli_block_mask_gpu(self.rows, nqb, nkb, density=self.density, seed=self.seed,
+                                                q_block_offset=qbo, device=device)
         return bernoulli_block_mask(self.rows, nqb, nkb, density=self.density, seed=self.seed,
                                     q_block_offset=qbo)
 
