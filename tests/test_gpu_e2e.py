@@ -1,22 +1,29 @@
-"""End to end at the configs[4] architecture: the Qwen3-4B-shaped model (36 layers, 32Q/8KV, head dim
-128, BigBird in layers 0-17, dense causal in 18-35, all on the HIP kernels, paged KV cache) against
-the same weights with every attention layer on the fp32 dense-masked oracle.  Prompt shortened to
-2048 tokens and batch 1 so the oracle's dense scores stay small; the logit difference is printed."""
-import copy
+"""End to end at configs[4]: the Qwen3-4B architecture (36 layers, hidden 2560, 32Q/8KV, head dim
+128, SwiGLU 9728, vocab 151936, random init), BigBird (window 3, global 2, random 3, block 64) in
+layers 0-17 and dense causal in 18-35, batch 8, an 8192-token prompt, paged KV cache.
+
+* Per-layer teacher forcing: every attention layer runs a twin backend that computes the HIP kernel
+  and the reference's dense-masked arithmetic (fp32, row-chunked) on the same q/k/v and passes the
+  oracle's result on, so each layer's kernel sees exactly the oracle path's inputs.  Every layer's
+  attention core, in the prompt forward and in paged decode steps, must meet the kernel tolerance
+  against the fp32 oracle: mean-abs 2e-3, and every element within max(2e-2, one bf16 ulp of the
+  oracle value, at most 2^-7 of it) -- the deeper layers of the random-init model produce attention outputs above 4,
+  where one bf16 ulp (3.1e-2) is already wider than the absolute 2e-2.
+* The logit max-abs difference of the all-kernel model against that oracle path (the reference's
+  sparse path, which cannot run on this machine) is reported at the stated size
+  (``sparse_llm/common/benchmark/generation.py:232-271`` defines the metrics).
+"""
 import sys
 
 import pytest
 import torch
-from transformers.cache_utils import DynamicCache
 
-from sparseattentioninfer_amd.qwen3 import PagedKVCache, replace_qwen3_attention_with_sparse
+from sparseattentioninfer_amd.qwen3 import PagedKVCache
 from sparseattentioninfer_amd.qwen3.runtime import build_model, qwen3_config
-from tests import oracle_backend
-from tests.helpers import assert_close_bf16
+from tests.helpers import MEAN_ABS
+from tests.twin_backend import TwinBackend
 
 pytestmark = pytest.mark.gpu
-
-ORACLE = oracle_backend.register()
 
 
 def _say(msg):
@@ -24,47 +31,64 @@ def _say(msg):
     sys.stdout.flush()
 
 
+def _use(model, backend_for_layer):
+    for layer in model.model.layers:
+        a = layer.self_attn
+        be = backend_for_layer(a.layer_idx)
+        a.sparse_backends = {"twin": be}
+        a.backend_candidates = ["twin"]
+        a.backend_name = "twin"
+        a.sparse_backend = be
+
+
 @torch.no_grad()
-def test_qwen3_4b_architecture_logits_track_the_oracle():
-    _say("[e2e] building Qwen3-4B-architecture model")
+def test_configs_4_stated_size_teacher_forced_layers_and_logits():
+    B, T, steps = 8, 8192, 2
+    _say(f"[e2e] Qwen3-4B architecture, B={B}, prompt {T}")
     cfg = qwen3_config(sparse_layers=range(18), pattern="seeded_bigbird", block_size=64, window=3,
                        global_blocks=2, random_blocks=3, seed=11)
-    hip = build_model(cfg, device="cuda", dtype=torch.bfloat16, seed=0)
-    ref = copy.deepcopy(hip)
-    replace_qwen3_attention_with_sparse(ref.model, backend_name=ORACLE, block_size=64)
-    for layer in ref.model.layers:                    # keep the sparse/dense split of the original
-        i = layer.self_attn.layer_idx
-        layer.self_attn.sparse_pattern = hip.model.layers[i].self_attn.sparse_pattern
-    # layer 0 sees identical inputs in both models: its attention core (the o_proj input) must meet the
-    # kernel tolerance at the full shape; deeper layers inherit bf16 differences from below
-    core = {}
+    model = build_model(cfg, device="cuda", dtype=torch.bfloat16, seed=0)
+    assert {layer.self_attn.pattern_name for layer in model.model.layers} == {"seeded_bigbird", "dense"}
+    hip_backends = [layer.self_attn.sparse_backend for layer in model.model.layers]
+    ids = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(12)).cuda()
 
-    def keep(name):
-        def hook(module, inputs, output):   # returns None: the module's output is left alone
-            core.setdefault(name, inputs[0].clone())
-        return hook
+    # oracle path, every layer's kernel checked on the oracle path's inputs
+    twins = [TwinBackend("oracle") for _ in model.model.layers]
+    _use(model, lambda i: twins[i])
+    cache = PagedKVCache(cfg.num_hidden_layers, T + steps + 1, page=64, shuffle_seed=3)
+    ref_logits, inputs = [], []
+    nxt = None
+    for s in range(steps + 1):
+        inp = ids if s == 0 else nxt[:, None]
+        lg = model(input_ids=inp, past_key_values=cache, use_cache=True, logits_to_keep=1).logits[:, -1].float()
+        ref_logits.append(lg)
+        nxt = lg.argmax(-1)
+        inputs.append(nxt)
+        recs = [t.records[-1] for t in twins]
+        worst_max = max(r["max_abs"] for r in recs)
+        worst_mean = max(r["mean_abs"] for r in recs)
+        worst_bound = max(r["bound"] for r in recs)
+        scale = max(r["out_scale"] for r in recs)
+        _say(f"[e2e] {'prompt' if s == 0 else f'decode step {s}'}: worst layer attention max-abs {worst_max:.3e}, "
+             f"mean-abs {worst_mean:.3e}, error / max(2e-2, 2^-7 |oracle|) {worst_bound:.3f} over {len(recs)} layers "
+             f"(largest attention output {scale:.2f})")
+        for i, r in enumerate(recs):
+            assert r["bound"] <= 1.0 and r["mean_abs"] <= MEAN_ABS, (s, i, r)
+    assert all(t.last_kernel == "decode" for t in twins)
+    del cache
+    torch.cuda.empty_cache()
 
-    hip.model.layers[0].self_attn.o_proj.register_forward_hook(keep("hip"))
-    ref.model.layers[0].self_attn.o_proj.register_forward_hook(keep("ref"))
-    ids = torch.randint(0, cfg.vocab_size, (1, 2048), generator=torch.Generator().manual_seed(12)).cuda()
-    c_hip = PagedKVCache(cfg.num_hidden_layers, 2100, page=64, shuffle_seed=3)
-    c_ref = DynamicCache(config=ref.config)
-    worst = 0.0
-    for step in range(4):                             # prompt, then teacher-forced decode steps
-        inp = ids if step == 0 else nxt[:, None]
-        la = hip(input_ids=inp, past_key_values=c_hip, use_cache=True, logits_to_keep=1).logits[:, -1].float()
-        lb = ref(input_ids=inp, past_key_values=c_ref, use_cache=True, logits_to_keep=1).logits[:, -1].float()
-        diff, scale = (la - lb).abs().max().item(), lb.abs().max().item()
-        agree = bool((la.argmax(-1) == lb.argmax(-1)).all())
-        _say(f"[e2e] step {step}: logits max-abs diff {diff:.4e}, logit scale {scale:.4e}, top-1 agree {agree}")
-        worst = max(worst, diff / scale)
-        nxt = lb.argmax(-1)
-        if step == 0:
-            max_abs, mean_abs = assert_close_bf16(core["hip"], core["ref"], "layer 0 attention")
-            _say(f"[e2e] layer 0 attention core: max-abs {max_abs:.3e}, mean-abs {mean_abs:.3e}")
-    kinds = {layer.self_attn.pattern_name for layer in hip.model.layers}
-    assert kinds == {"seeded_bigbird", "dense"}
-    assert all(layer.self_attn.sparse_backend.last_kernel == "decode" for layer in hip.model.layers)
-    # 36 layers of bf16 activations: the relative logit difference measured here is 4-5 %; the bound
-    # leaves room for other seeds without hiding a broken layer (which the layer-0 check would catch)
-    assert worst <= 0.10, f"relative logit difference {worst:.3e}"
+    # the all-kernel model against the oracle path, teacher-forced with the oracle path's tokens
+    _use(model, lambda i: hip_backends[i])
+    cache = PagedKVCache(cfg.num_hidden_layers, T + steps + 1, page=64, shuffle_seed=3)
+    for s in range(steps + 1):
+        inp = ids if s == 0 else inputs[s - 1][:, None]
+        lg = model(input_ids=inp, past_key_values=cache, use_cache=True, logits_to_keep=1).logits[:, -1].float()
+        ref = ref_logits[s]
+        diff, scale = (lg - ref).abs().max().item(), ref.abs().max().item()
+        agree = (lg.argmax(-1) == ref.argmax(-1)).float().mean().item()
+        _say(f"[e2e] {'prompt' if s == 0 else f'decode step {s}'}: logit max-abs diff {diff:.4e} "
+             f"(logit scale {scale:.3e}), top-1 agreement {agree:.3f}")
+        assert torch.isfinite(lg).all()
+        # bf16 activations over 36 layers compound; each layer is held to the kernel tolerance above
+        assert diff <= 0.15 * max(1.0, scale), (s, diff, scale)

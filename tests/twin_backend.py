@@ -1,0 +1,87 @@
+"""Test-only backend that runs the HIP kernels and the oracle on the same q/k/v at every call.
+
+Each call computes the HIP backend's output and the reference's dense-masked arithmetic over
+the same block schedule (``oracle.attention.masked_sdpa_blockwise``: row-chunked, fp32, so it
+runs at 8192-token prompts with batch 8), records the max-abs / mean-abs difference and returns
+one of the two:
+
+* ``returns="oracle"`` -- every later layer sees the oracle path's activations, so each
+  recorded difference is that layer's attention core alone, teacher-forced (the HIP kernel on
+  exactly the inputs the oracle path produced);
+* ``returns="hip"`` -- the model runs on the kernels, the oracle only checks.
+
+Paged decode goes through the HIP backend's ``forward_paged`` and the oracle reads the same
+pages back with ``store.gather()``.
+"""
+from __future__ import annotations
+
+import torch
+
+from oracle import attention as oa
+from oracle import csr as ocsr
+from sparseattentioninfer_amd.attention import AttentionBackend, HipBlockSparseBackend, register_backend
+from sparseattentioninfer_amd.patterns.base import kv_block_list_to_pairs
+
+NAME = "twin_hip_oracle"
+
+
+def _oracle(q, k, v, pattern):
+    B, H, T_q, _ = q.shape
+    T_k = k.size(2)
+    if pattern.kind == "dense":
+        bs = 64
+        nqb, nkb = -(-T_q // bs), -(-T_k // bs)
+        bm = torch.ones(1, nqb, nkb, dtype=torch.bool)
+    else:
+        pairs, offsets = pattern.block_pairs, pattern.block_pair_offsets
+        if pairs is None:
+            pairs, offsets = kv_block_list_to_pairs(pattern.kv_block_list)
+        bs = pattern.block_size
+        bm = torch.from_numpy(ocsr.csr_to_block_mask(pairs.cpu().numpy(), offsets.cpu().numpy(), -(-T_k // bs)))
+    return oa.masked_sdpa_blockwise(q, k, v, bm, bs, q_offset=T_k - T_q)          # fp32
+
+
+class TwinBackend(AttentionBackend):
+    supports_gqa = True
+
+    def __init__(self, returns: str = "oracle"):
+        assert returns in ("oracle", "hip")
+        self.returns = returns
+        self.hip = HipBlockSparseBackend()
+        self.records: list[dict] = []
+
+    @property
+    def actual_backend(self) -> str:
+        return NAME
+
+    @property
+    def last_kernel(self):
+        return self.hip.last_kernel
+
+    def _pick(self, got, want, T_q, T_k, kind):
+        """Records the kernel's error against the fp32 oracle: max-abs, mean-abs and ``bound`` = the
+        worst ratio of an element's error to max(2e-2, 2^-7 |oracle|), i.e. the BASELINE absolute
+        tolerance, widened to one bf16 ulp (of the binade's top) where the output exceeds 2.56 (one bf16
+        ulp of a value in [4, 8) is already 3.1e-2)."""
+        d = (got.float() - want).abs()
+        allow = torch.clamp(want.abs() * 2.0 ** -7, min=2e-2)
+        self.records.append({"T_q": T_q, "T_k": T_k, "kind": kind, "max_abs": d.max().item(),
+                             "mean_abs": d.mean().item(), "bound": (d / allow).max().item(),
+                             "out_scale": want.abs().max().item()})
+        return want.to(got.dtype) if self.returns == "oracle" else got
+
+    def forward(self, q, k, v, pattern):
+        got = self.hip.forward(q, k, v, pattern)
+        return self._pick(got, _oracle(q, k, v, pattern), q.size(2), k.size(2), pattern.kind)
+
+    def forward_paged(self, q, store, pattern):
+        got = self.hip.forward_paged(q, store, pattern)
+        k, v = store.gather()
+        return self._pick(got, _oracle(q, k, v, pattern), q.size(2), k.size(2), pattern.kind)
+
+
+def register(returns: str = "oracle") -> str:
+    name = f"{NAME}_{returns}"
+    register_backend(name, type(f"TwinBackend_{returns}", (TwinBackend,), {"__init__":
+                     lambda self: TwinBackend.__init__(self, returns)}))
+    return name
