@@ -68,6 +68,30 @@ def parse():
     return ap.parse_args()
 
 
+SETTLE_S = 0.25      # sustained launches before the warm-up steps (see _settle)
+SETTLE_MAX = 5000
+
+
+def _settle(launch, seconds: float = SETTLE_S) -> int:
+    """Launches the kernel back to back for ``seconds`` (at most SETTLE_MAX launches), untimed.
+
+    Measured on MI355X: after even 50 ms without MFMA load, the first two or three prefill launches
+    run at full clock, the next ones 15-45 % slower (the power controller's response to the load
+    step) and the rate recovers over about 60-100 launches (30-50 ms) to its sustained level.  The
+    kernel legs settle first, then take their W warm-up and K timed launches, so they report the
+    sustained rate; the prefill leg also reports its first W + K launches before settling."""
+    import torch
+    n = 0
+    t0 = time.perf_counter()
+    while n < SETTLE_MAX and (n % 32 or time.perf_counter() - t0 < seconds):
+        launch()
+        n += 1
+        if n % 32 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
+
+
 def _events_time(launch, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -119,8 +143,11 @@ def run_prefill(args, dev):
     from sparseattentioninfer_amd import ops
     (q, k, v, pairs, offsets, bm), info, flops = prefill_workload(dev)
     launch = ops.prepare_prefill(q, k, v, pairs, offsets, BS)
+    _, ev_cold = _events_time(launch, args.steps, args.warmup)      # first W + K launches, unsettled
+    settle = _settle(launch)
     wall, ev = _events_time(launch, args.steps, args.warmup)
     avg = ev / args.steps
+    info = {**info, "settle_launches": settle, "kernel_us_before_settle": round(ev_cold / args.steps * 1e6, 2)}
     res = {
         "value": flops / (wall / args.steps) / 1e12,
         "ms_per_step": wall / args.steps * 1e3,
@@ -165,9 +192,10 @@ def run_prefill_bernoulli(args, dev):
     from sparseattentioninfer_amd import ops
     (q, k, v, pairs, offsets), info, flops = bernoulli_workload(dev)
     launch = ops.prepare_prefill(q, k, v, pairs, offsets, BS)
+    settle = _settle(launch)
     wall, ev = _events_time(launch, args.steps, args.warmup)
     avg = ev / args.steps
-    return {**info, "steps": args.steps, "warmup": args.warmup, "ms_per_step": wall / args.steps * 1e3,
+    return {**info, "steps": args.steps, "warmup": args.warmup, "settle_launches": settle, "ms_per_step": wall / args.steps * 1e3,
             "kernel_us": avg * 1e6, "tflops": flops / (wall / args.steps) / 1e12, "flops_per_launch": flops,
             "roofline": {"bound": "mfma", "achieved": flops / avg / 1e12, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None}}
@@ -237,6 +265,24 @@ def decode_workload(dev):
     return t, info, kv_bytes + io_bytes + idx_bytes
 
 
+def stream_read_ceiling(dev, nbytes: int = 4 << 30, reps: int = 20) -> dict:
+    """HBM streaming-read rate of this GPU, measured in the same run (``sa_stream_read``: every
+    byte of a 4 GiB buffer read once per launch), the practical ceiling of a memory-bound kernel."""
+    import torch
+    from sparseattentioninfer_amd import _lib
+    lib = _lib.load()
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    sink = torch.empty(int(lib.sa_stream_read_workgroups()), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def launch():
+        _lib.check("sa_stream_read", lib.sa_stream_read(buf.data_ptr(), nbytes, sink.data_ptr(), stream))
+
+    _, ev = _events_time(launch, reps, 5)
+    del buf
+    return {"gbs": nbytes / (ev / reps) / 1e9, "bytes": nbytes, "launches": reps}
+
+
 def run_decode(args, dev):
     from sparseattentioninfer_amd import ops
     (q, kp, vp, table, lens, sel, sel_off), info, nbytes = decode_workload(dev)
@@ -244,6 +290,7 @@ def run_decode(args, dev):
     best = None
     for splits in ([args.decode_splits] if args.decode_splits else [1, 2]):
         launch = ops.prepare_paged_decode(q, kp, vp, table, lens, sel, sel_off, num_splits=splits)
+        _settle(launch)
         wall, ev = _events_time(launch, steps, max(args.warmup, 10))
         cand = (ev / steps, wall / steps, splits)
         if best is None or cand[0] < best[0]:
@@ -251,6 +298,9 @@ def run_decode(args, dev):
     avg, per_step, splits = best
     gbs = nbytes / avg / 1e9
     info["num_splits"] = splits
+    ceiling = stream_read_ceiling(dev)
+    info["stream_read_ceiling_gbs"] = ceiling["gbs"]
+    info["frac_of_stream_read"] = gbs / ceiling["gbs"]
     return {
         **info,
         "steps": steps,
@@ -408,6 +458,20 @@ def main():
             "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True, "scaling": "weak",
             "vs_baseline": None, "dtype": "bf16",
             "data": "synthetic: seeded N(0,1) q/k/v (q,k scaled per head dim by U(0.5,2)), seeded BigBird blocks"}
+    # The end-to-end leg runs first; each kernel leg then settles (_settle) before its W warm-up and
+    # K timed launches.
+    e2e_done = None
+    if not args.no_e2e and args.only == "all":
+        try:
+            e2e = run_e2e(args, dev)
+            e2e_done = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in e2e.items()}
+        except Exception as exc:   # the kernel figures below stay valid; say what failed
+            e2e_done = {"error": f"{type(exc).__name__}: {exc}"}
+            print(f"e2e leg failed: {exc!r}", file=sys.stderr)
+        torch.cuda.empty_cache()
+    if args.only == "all":
+        line["leg_order"] = ("e2e, " if e2e_done is not None else "") + \
+            "configs[2] prefill, configs[1] prefill, decode, pattern build, cpu baseline"
     pre = None
     if args.only in ("all", "prefill"):
         pre = run_prefill(args, dev)
@@ -434,13 +498,8 @@ def main():
     if args.only == "all":
         pb = run_pattern_build(dev)
         line["pattern_build"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pb.items()}
-    if not args.no_e2e and args.only == "all":
-        try:
-            e2e = run_e2e(args, dev)
-            line["e2e"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in e2e.items()}
-        except Exception as exc:   # the kernel figures above stay valid; say what failed
-            line["e2e"] = {"error": f"{type(exc).__name__}: {exc}"}
-            print(f"e2e leg failed: {exc!r}", file=sys.stderr)
+    if e2e_done is not None:
+        line["e2e"] = e2e_done
     if pre is not None and not args.no_cpu_baseline:
         cb = cpu_baseline(pre, args.cpu_seconds)
         cb["value"] = round(cb["value"], 5)

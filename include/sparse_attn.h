@@ -261,6 +261,16 @@ int sa_decode_noalloc(int dtype,
 int64_t sa_decode_noalloc_scratch_bytes(void);
 
 /*
+ * Measurement aid, no counterpart in the reference: reads `bytes` (a multiple
+ * of 16) at src once with 16-byte loads from sa_stream_read_workgroups()
+ * workgroups (8 per CU) and writes one xor-folded word per workgroup to sink
+ * (that many uint32).  Its rate is the HBM streaming-read ceiling that the
+ * memory-bound decode kernel is compared with.
+ */
+int sa_stream_read(const void* src, int64_t bytes, uint32_t* sink, void* stream);
+int sa_stream_read_workgroups(void);
+
+/*
  * Fused elementwise stages of one decode step of a Qwen3 decoder layer, for the
  * graph-captured end-to-end decode (callers of the attention path, not the
  * attention itself).  They keep Hugging Face's arithmetic: fp32 inside,

@@ -134,11 +134,20 @@ def test_skinny_gemm_fp16(M, N, K):
 def test_gemm_skinny_swiglu(M, I, K, dtype):
     """Gate|up product with the SwiGLU in its epilogue, on interleaved weights, gives the bits of the
     product on the concatenated weights followed by sa_swiglu (both products on the matrix-core
-    kernel: 2I >= 6144 columns); with a ragged last column tile and a single 128-wide K stage."""
+    kernel, which holds for 2I >= 24 columns per CU); with a ragged last column tile and a single
+    128-wide K stage."""
     _say(f"[layer-ops] gemm_skinny_swiglu M={M} I={I} K={K} {dtype}")
     x = _rand(M, K, seed=130 + M).to(dtype)
     gate = _rand(I, K, seed=140 + I % 97, scale=0.05).to(dtype)
     up = _rand(I, K, seed=150 + I % 97, scale=0.05).to(dtype)
     fused = ops.gemm_skinny_swiglu(x, ops.interleave_gate_up(gate, up))
     two = ops.swiglu(ops.gemm_skinny(x, torch.cat([gate, up], 0).contiguous()))
-    assert torch.equal(fused, two)
+    # The fused product always runs on the matrix-core kernel; the plain product does when K is a
+    # multiple of 128 and N = 2I >= 24 columns per CU (layer_ops.hip's dispatch), which depends on the
+    # part's CU count.  Same kernel: the same bits; otherwise the dot-product kernel sums K in another
+    # order, and the results agree to a bf16/fp16 ulp of the SwiGLU output.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    if K % 128 == 0 and 2 * I >= 24 * cus:
+        assert torch.equal(fused, two)
+    else:
+        assert_within_ulps(fused, two, 1, "fused vs two-step SwiGLU (different product kernels)")
