@@ -80,7 +80,19 @@ struct PrefillArgs {
   int q_offset;
   float scale_log2;  // sm_scale * log2(e)
   unsigned int* counter;  // persistent mode: 2 zeroed counters (next item, finished workgroups)
+  // Work-item decoding without integer division: per_tile = R * B * head_splits, and
+  // floor((2^32 - 1) / d) for d = per_tile, R, head_splits (see fast_div).
+  int per_tile;
+  uint32_t mul_tile, mul_R, mul_hs;
 };
+
+// floor(n / d) for n < 2^32 and 1 <= d < 2^32, given m = floor((2^32 - 1) / d): m >= (2^32 - d)/d,
+// so the high word of n*m is floor(n/d) or one less, and one compare corrects it.
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t d, uint32_t m) {
+  uint32_t q = __umulhi(n, m);
+  q += (n - q * d >= d) ? 1u : 0u;
+  return q;
+}
 
 __device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(const void* p) {
   return (__attribute__((address_space(3))) void*)(p);
@@ -291,10 +303,26 @@ struct Prefill {
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   }
 
-  // B operand of S^T = K Q^T from a wave's staged Q ([cc][lane] 16 bytes: lane l holds row
-  // l32, columns 16cc + 8g .. +7).
-  static __device__ __forceinline__ u32x4 qfrag(const char* sQw, int lane, int cc) {
-    return *reinterpret_cast<const u32x4*>(sQw + cc * 1024 + lane * 16);
+  // B operand of S^T = K Q^T from a wave's staged Q, laid out like a staged K/V tile of 32
+  // rows: column group cg (32 columns) at cg*2048, row r at r*64, its 16-byte chunk c at
+  // position c ^ ((r >> 2) & 3).  Lane l needs row l32, columns 16cc + 8g .. +7 (chunk
+  // 2(cc & 1) + g of group cc/2), which is the K fragment offset of the same lane.
+  static __device__ __forceinline__ u32x4 qfrag(const char* sQw, const Frag& f, int cc) {
+    const int off = (cc & 1) ? (f.k0 ^ 32) : f.k0;
+    return *reinterpret_cast<const u32x4*>(sQw + 2048 * (cc >> 1) + off);
+  }
+
+  // Direct loads of this wave's 32 rows of Q into that layout: load k fills rows 16(k / NCG) ..
+  // +15 of column group k % NCG, lane i row 16(k / NCG) + i/4, columns 32(k % NCG) + dma_col(i)
+  // (16 rows x 64 bytes per instruction, as for K and V).  Rows past T_q read row T_q - 1.
+  static __device__ __forceinline__ void load_q(const PrefillArgs& a, const elem_t* qh, int row0, char* sQw,
+                                                int lane) {
+#pragma unroll
+    for (int k = 0; k < 2 * NCG; ++k) {
+      const int cg = k % NCG, rb = k / NCG;
+      const int grow = min(row0 + 16 * rb + (lane >> 2), a.Tq - 1);
+      load_lds16(qh + (int64_t)grow * a.q_st + 32 * cg + dma_col(lane), lds_addr(sQw + cg * 2048 + rb * 1024));
+    }
   }
 
   // ---- work items ---------------------------------------------------------------------
@@ -765,7 +793,7 @@ struct Prefill {
     ld.nv = 0;
     if (lk.v1 < lk.n_items && lk.n_1 <= RC) {
       int qt, r, hs, b;
-      decode_item(a, lk.v1, qt, r, hs, b);
+      decode_item_uniform(a, lk.v1, qt, r, hs, b);
       const int32_t* src = a.pairs + r * a.pairs_stride + lk.e0_1;
 #pragma unroll
       for (int u = 0; u < RPT; ++u)
@@ -820,12 +848,8 @@ struct Prefill {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const Item it = LOOK ? setup_base(a, qt, r, hs, b, lk->e0, lk->n_ent) : setup(a, qt, r, hs, b, s_row, s_mask);
-    const char* sQw = sQ + wave * WAVE_BYTES;
-    {  // Q^T operand of this wave into LDS, in fragment order
-      const elem_t* qs = q_src(a, it);
-#pragma unroll
-      for (int cc = 0; cc < D / 16; ++cc) load_lds16(qs + 16 * cc, lds_addr(sQw + cc * 1024));
-    }
+    char* sQw = sQ + wave * WAVE_BYTES;
+    load_q(a, it.qb, it.q_row0, sQw, lane);  // Q^T operand of this wave into LDS
     const Frag f(lane);
     const DmaLane dl(a, lane);
     // lim of tile kt: min(q_abs, T_k - 1) - kt*KT - 8g (past the tile when no key is masked)
@@ -881,7 +905,7 @@ struct Prefill {
     if (has_cur) {
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
-        const u32x4 qv = qfrag(sQw, lane, cc);
+        const u32x4 qv = qfrag(sQw, f, cc);
 #pragma unroll
         for (int j = 0; j < 2; ++j) S[j] = E::mfma32(kfrag(sK, f, j, cc), qv, S[j]);
       }
@@ -961,7 +985,7 @@ struct Prefill {
       // share of the VALU work.
       auto kfr = [&](int i) { return kfrag(cK, f, i & 1, i >> 1); };
       u32x4 kf[3] = {kfr(0), kfr(1), kfr(2)};
-      u32x4 qv[2] = {qfrag(sQw, lane, 0), qfrag(sQw, lane, 1)};
+      u32x4 qv[2] = {qfrag(sQw, f, 0), qfrag(sQw, f, 1)};
       Sx[0] = f32x16{};
       Sx[1] = f32x16{};
       float ls = 0.f;
@@ -974,7 +998,7 @@ struct Prefill {
       for (int i = 0; i < NQ; ++i) {
         Sx[i & 1] = E::mfma32(kf[i % 3], qv[(i >> 1) & 1], Sx[i & 1]);
         if (i + 3 < NQ) kf[i % 3] = kfr(i + 3);
-        if ((i & 1) && (i >> 1) + 2 < D / 16) qv[(i >> 1) & 1] = qfrag(sQw, lane, (i >> 1) + 2);
+        if ((i & 1) && (i >> 1) + 2 < D / 16) qv[(i >> 1) & 1] = qfrag(sQw, f, (i >> 1) + 2);
 #pragma unroll
         for (int u = 0; u < PE; u += 2) {
           const int x = PE * i + u;
@@ -1029,21 +1053,34 @@ struct Prefill {
     epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
   }
 
-  // Item index -> (qt, r, hs, b), the heaviest (latest) query tiles first.
+  // Item index -> (qt, r, hs, b), the heaviest (latest) query tiles first.  Per lane: v may
+  // differ between lanes (the startup reads two items' offsets in two lanes).
   static __device__ __forceinline__ void decode_item(const PrefillArgs& a, int v, int& qt, int& r, int& hs, int& b) {
-    const int per_tile = a.R * a.B * a.head_splits;
-    qt = a.ntq - 1 - v / per_tile;
-    int rem = v % per_tile;
-    r = rem % a.R;
-    rem /= a.R;
-    hs = rem % a.head_splits;
-    b = rem / a.head_splits;
+    const uint32_t t = fast_div((uint32_t)v, (uint32_t)a.per_tile, a.mul_tile);
+    qt = a.ntq - 1 - (int)t;
+    const uint32_t rem = (uint32_t)v - t * (uint32_t)a.per_tile;  // (r, hs, b) with r fastest
+    const uint32_t t2 = fast_div(rem, (uint32_t)a.R, a.mul_R);
+    r = (int)(rem - t2 * (uint32_t)a.R);
+    const uint32_t t3 = fast_div(t2, (uint32_t)a.head_splits, a.mul_hs);
+    hs = (int)(t2 - t3 * (uint32_t)a.head_splits);
+    b = (int)t3;
+  }
+
+  // decode_item for an item index that is the same in every lane of the wave: the results are
+  // moved to scalar registers, and so is every address derived from them.
+  static __device__ __forceinline__ void decode_item_uniform(const PrefillArgs& a, int v, int& qt, int& r, int& hs,
+                                                             int& b) {
+    decode_item(a, __builtin_amdgcn_readfirstlane(v), qt, r, hs, b);
+    qt = __builtin_amdgcn_readfirstlane(qt);
+    r = __builtin_amdgcn_readfirstlane(r);
+    hs = __builtin_amdgcn_readfirstlane(hs);
+    b = __builtin_amdgcn_readfirstlane(b);
   }
 
   static __device__ __forceinline__ void process(const PrefillArgs& a, int v, char* sKV, char* sQ,
                                                  int32_t* s_row, int32_t* s_mask) {
     int qt, r, hs, b;
-    decode_item(a, v, qt, r, hs, b);
+    decode_item_uniform(a, v, qt, r, hs, b);
     if constexpr (PIPE)
       item_pipelined<false>(a, qt, r, hs, b, sKV, sQ, s_row, s_mask, nullptr);
     else
@@ -1083,7 +1120,7 @@ struct Prefill {
       const int e0 = s_off[0], n = s_off[1] - e0;
       if (v < n_items && n <= RC) {
         int qt, r, hs, b;
-        decode_item(a, v, qt, r, hs, b);
+        decode_item_uniform(a, v, qt, r, hs, b);
         for (int x = tid; x < n; x += NT) {
           s_row[x] = a.pairs[r * a.pairs_stride + e0 + x];
           if (SUB) s_mask[x] = a.tile_masks[r * a.masks_stride + e0 + x];
@@ -1110,7 +1147,7 @@ struct Prefill {
       lk.off_dst = s_off + 2 * ((i + 2) & 3);
       lk.vid_dst = s_vid + ((i + 3) & 3);
       int qt, r, hs, b;
-      decode_item(a, v, qt, r, hs, b);
+      decode_item_uniform(a, v, qt, r, hs, b);
       item_pipelined<true>(a, qt, r, hs, b, sKV, sQ, s_row + (i & 1) * RC, SUB ? s_mask + (i & 1) * RC : s_mask,
                            &lk);
     }
@@ -1294,6 +1331,10 @@ extern "C" int sa_prefill(int dtype,
   a.tpb_log2 = block_size == 128 ? 1 : 0;
   a.q_offset = q_offset;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.per_tile = a.R * B * a.head_splits;
+  a.mul_tile = 0xFFFFFFFFu / (uint32_t)a.per_tile;
+  a.mul_R = 0xFFFFFFFFu / (uint32_t)a.R;
+  a.mul_hs = 0xFFFFFFFFu / (uint32_t)a.head_splits;
   if (workspace && workspace_bytes < sa_prefill_workspace_bytes())
     return set_error(SA_E_WORKSPACE, "sa_prefill: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
                      (long long)sa_prefill_workspace_bytes());
