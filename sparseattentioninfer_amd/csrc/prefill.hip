@@ -84,7 +84,21 @@ struct PrefillArgs {
   // floor((2^32 - 1) / d) for d = per_tile, R, head_splits (see fast_div).
   int per_tile;
   uint32_t mul_tile, mul_R, mul_hs;
+  // Persistent launches (row_order) take the query tiles from q_split up latest first with all
+  // rows of a tile together, then the tiles below q_split row by row, the CSR rows in
+  // descending order of retained blocks (s_row_rank), latest first within a row: the lightest
+  // items come last, so workgroups run out of work at nearly the same time, while most of the
+  // launch keeps every row's tiles in flight.  head_items = (ntq - q_split) * per_tile;
+  // per_group = q_split * bhs items per row below q_split; bhs = B * head_splits.
+  int row_order;
+  int nqb;
+  int q_split, head_items, per_group, bhs;
+  uint32_t mul_group, mul_bhs;
 };
+
+// CSR rows of a persistent launch in descending order of retained blocks (row_order).
+constexpr int MAX_ORDERED_ROWS = 256;
+__shared__ int s_row_rank[MAX_ORDERED_ROWS];
 
 // floor(n / d) for n < 2^32 and 1 <= d < 2^32, given m = floor((2^32 - 1) / d): m >= (2^32 - d)/d,
 // so the high word of n*m is floor(n/d) or one less, and one compare corrects it.
@@ -1053,17 +1067,49 @@ struct Prefill {
     epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
   }
 
-  // Item index -> (qt, r, hs, b), the heaviest (latest) query tiles first.  Per lane: v may
-  // differ between lanes (the startup reads two items' offsets in two lanes).
+  // Item index -> (qt, r, hs, b).  Per lane: v may differ between lanes (the startup reads two
+  // items' offsets in two lanes).  Without row_order: query tiles latest first, all rows of a
+  // tile together; with it: row by row (s_row_rank), latest query tiles first within a row.
   static __device__ __forceinline__ void decode_item(const PrefillArgs& a, int v, int& qt, int& r, int& hs, int& b) {
-    const uint32_t t = fast_div((uint32_t)v, (uint32_t)a.per_tile, a.mul_tile);
-    qt = a.ntq - 1 - (int)t;
-    const uint32_t rem = (uint32_t)v - t * (uint32_t)a.per_tile;  // (r, hs, b) with r fastest
-    const uint32_t t2 = fast_div(rem, (uint32_t)a.R, a.mul_R);
-    r = (int)(rem - t2 * (uint32_t)a.R);
-    const uint32_t t3 = fast_div(t2, (uint32_t)a.head_splits, a.mul_hs);
-    hs = (int)(t2 - t3 * (uint32_t)a.head_splits);
+    uint32_t rem;
+    if (a.row_order && v >= a.head_items) {
+      const uint32_t w = (uint32_t)(v - a.head_items);
+      const uint32_t k = fast_div(w, (uint32_t)a.per_group, a.mul_group);
+      r = s_row_rank[k];
+      const uint32_t rq = w - k * (uint32_t)a.per_group;
+      const uint32_t t = fast_div(rq, (uint32_t)a.bhs, a.mul_bhs);
+      qt = a.q_split - 1 - (int)t;
+      rem = rq - t * (uint32_t)a.bhs;  // (hs, b) with hs fastest
+    } else {
+      const uint32_t t = fast_div((uint32_t)v, (uint32_t)a.per_tile, a.mul_tile);
+      qt = a.ntq - 1 - (int)t;
+      const uint32_t rt = (uint32_t)v - t * (uint32_t)a.per_tile;  // (r, hs, b) with r fastest
+      const uint32_t t2 = fast_div(rt, (uint32_t)a.R, a.mul_R);
+      r = (int)(rt - t2 * (uint32_t)a.R);
+      rem = t2;
+    }
+    const uint32_t t3 = fast_div(rem, (uint32_t)a.head_splits, a.mul_hs);
+    hs = (int)(rem - t3 * (uint32_t)a.head_splits);
     b = (int)t3;
+  }
+
+  // Ranks the CSR rows by retained blocks (descending, ties by row) into s_row_rank; callers
+  // barrier before the first decode_item.
+  static __device__ __forceinline__ void rank_rows(const PrefillArgs& a, int* s_len) {
+    for (int r = threadIdx.x; r < a.R; r += NT) {
+      const int32_t* o = a.offsets + r * a.offsets_stride;
+      s_len[r] = o[a.nqb] - o[0];
+    }
+    __syncthreads();
+    for (int r = threadIdx.x; r < a.R; r += NT) {
+      const int len = s_len[r];
+      int rank = 0;
+      for (int u = 0; u < a.R; ++u) {
+        const int lu = s_len[u];
+        rank += (lu > len || (lu == len && u < r)) ? 1 : 0;
+      }
+      s_row_rank[rank] = r;
+    }
   }
 
   // decode_item for an item index that is the same in every lane of the wave: the results are
@@ -1180,6 +1226,7 @@ struct Prefill {
     // Persistent: claim items from a counter until none is left.  The last workgroup to
     // finish resets the counter pair to zero for the next launch on the stream.  The
     // barriers also separate one item's epilogue (LDS staging) from the next item's loads.
+    if (a.row_order) rank_rows(a, reinterpret_cast<int*>(sKV));  // K/V buffers are free here
     if constexpr (PIPE) {
       run_lookahead(a, n_items, sKV, sQ, s_row, s_mask);
     } else {
@@ -1332,6 +1379,18 @@ extern "C" int sa_prefill(int dtype,
   a.q_offset = q_offset;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.per_tile = a.R * B * a.head_splits;
+  a.nqb = nqb;
+  a.row_order = (workspace != nullptr && csr_rows <= MAX_ORDERED_ROWS) ? 1 : 0;
+  a.bhs = B * a.head_splits;
+  a.q_split = 0;
+  if (a.row_order) {  // tail of about four items per persistent workgroup
+    const int64_t tail = 4 * (int64_t)num_cus();
+    a.q_split = (int)std::min<int64_t>(a.ntq, ceil_div(tail, a.per_tile));
+  }
+  a.head_items = (a.ntq - a.q_split) * a.per_tile;
+  a.per_group = std::max(1, a.q_split * a.bhs);
+  a.mul_group = 0xFFFFFFFFu / (uint32_t)a.per_group;
+  a.mul_bhs = 0xFFFFFFFFu / (uint32_t)a.bhs;
   a.mul_tile = 0xFFFFFFFFu / (uint32_t)a.per_tile;
   a.mul_R = 0xFFFFFFFFu / (uint32_t)a.R;
   a.mul_hs = 0xFFFFFFFFu / (uint32_t)a.head_splits;
