@@ -573,7 +573,9 @@ struct Prefill {
       const int p = lane % NCH;
       const u32x4 w = *reinterpret_cast<const u32x4*>(stage + row * 2 * D + 16 * p);
       const int qrow = it.q_row0 + row;
-      if (qrow < a.Tq) *reinterpret_cast<u32x4*>(ob + (int64_t)qrow * a.o_st + 8 * (p ^ (row & (NCH - 1)))) = w;
+      // Non-temporal: O is not read again here, so it need not displace K/V lines in L2.
+      if (qrow < a.Tq)
+        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(ob + (int64_t)qrow * a.o_st + 8 * (p ^ (row & (NCH - 1)))));
     }
   }
 
