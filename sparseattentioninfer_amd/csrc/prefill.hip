@@ -1056,14 +1056,62 @@ struct Prefill {
       m_nxt = m_nn;
       vb_cur = vb_nxt;
     };
+    // O^T += V^T P^T of the tile in V buffer cV, nothing else (the last tile).
+    auto block_pv = [&](const char* cV) {
+      auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
+      u32x4 vf[2] = {vfr(0), vfr(1)};
+      __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        O[i % ND] = E::mfma32(vf[i & 1], P[i / (2 * ND)][(i / ND) & 1], O[i % ND]);
+        if (i + 2 < NP) vf[i & 1] = vfr(i + 2);
+      }
+    };
+
+    // The last tile: its probabilities and PV only.  There is no next tile, so no S^T half, no
+    // loads and no barrier (the one before the epilogue follows); the upper half's PV of this
+    // tile runs after it.
+    auto last_step = [&](f32x16 (&Sc)[2]) {
+      const int vb_prev = vb_cur == 0 ? 2 : vb_cur - 1;
+      if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, Sc);
+      const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
+      float ls = 0.f;
+      uint32_t pw[2][2][4];
+#pragma unroll
+      for (int x = 0; x < 32; x += 2) {
+        const int j = x >> 4, rr = x & 15;
+        const float p0 = fast_exp2(fmaf(Sc[j][rr], c, neg_m));
+        const float p1 = fast_exp2(fmaf(Sc[j][rr + 1], c, neg_m));
+        ls += p0 + p1;
+        pw[j][rr >> 3][(rr & 7) >> 1] = E::pack2f(p0, p1);
+      }
+      l_run += ls;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) P[j][h] = u32x4{pw[j][h][0], pw[j][h][1], pw[j][h][2], pw[j][h][3]};
+      if (!lag) block_pv(sV + vb_cur * TILE_BYTES);
+    };
+
     f32x16 Sn[2];
-    while (has_cur) {
-      step(std::integral_constant<int, 0>{}, S, Sn);
-      if (!has_cur) break;
-      step(std::integral_constant<int, 1>{}, Sn, S);
+    if (has_cur) {
+      bool odd = false;  // the last tile's scores are in Sn
+      while (has_nxt) {
+        step(std::integral_constant<int, 0>{}, S, Sn);
+        if (!has_nxt) {
+          odd = true;
+          break;
+        }
+        step(std::integral_constant<int, 1>{}, Sn, S);
+      }
+      if (odd) {
+        S[0] = Sn[0];
+        S[1] = Sn[1];
+      }
+      last_step(S);
+      // Upper half: PV of the last tile.
+      if (lag) block_pv(sV + vb_cur * TILE_BYTES);
     }
-    // Upper half: B of the last tile (its V buffer is not reloaded after the last step).
-    if (lag && pending) block_b(sV + (vb_cur == 0 ? 2 : vb_cur - 1) * TILE_BYTES, S);
     // Every wave is past its last read of the K/V buffers: they are free for the staging.
     __syncthreads();
     epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
