@@ -906,6 +906,8 @@ struct Prefill {
     uint32_t m_cur = 0u, m_nxt = 0u;
     bool has_cur = queue_pop(a, it, s_row, s_mask, q, kt_cur, m_cur);
     bool has_nxt = has_cur && queue_pop(a, it, s_row, s_mask, q, kt_nxt, m_nxt);
+    // Every wave is past the previous item's last reads of the K/V buffers.
+    if constexpr (LOOK) __syncthreads();
     if (has_cur) {
       load_k(kt_cur, 0);
       load_v(kt_cur, 0);
@@ -916,12 +918,15 @@ struct Prefill {
     wait_dma();
     if constexpr (LOOK) look_commit(*lk, ld);
     __syncthreads();
+    u32x4 Qr[D / 16];
+#pragma unroll
+    for (int cc = 0; cc < D / 16; ++cc) Qr[cc] = qfrag(sQw, f, cc);
     f32x16 S[2] = {f32x16{}, f32x16{}};  // scores of the current tile
     float mt_cur = -__builtin_inff();
     if (has_cur) {
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
-        const u32x4 qv = qfrag(sQw, f, cc);
+        const u32x4 qv = Qr[cc];
 #pragma unroll
         for (int j = 0; j < 2; ++j) S[j] = E::mfma32(kfrag(sK, f, j, cc), qv, S[j]);
       }
@@ -1001,7 +1006,6 @@ struct Prefill {
       // share of the VALU work.
       auto kfr = [&](int i) { return kfrag(cK, f, i & 1, i >> 1); };
       u32x4 kf[3] = {kfr(0), kfr(1), kfr(2)};
-      u32x4 qv[2] = {qfrag(sQw, f, 0), qfrag(sQw, f, 1)};
       Sx[0] = f32x16{};
       Sx[1] = f32x16{};
       float ls = 0.f;
@@ -1012,9 +1016,8 @@ struct Prefill {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NQ; ++i) {
-        Sx[i & 1] = E::mfma32(kf[i % 3], qv[(i >> 1) & 1], Sx[i & 1]);
+        Sx[i & 1] = E::mfma32(kf[i % 3], Qr[i >> 1], Sx[i & 1]);
         if (i + 3 < NQ) kf[i % 3] = kfr(i + 3);
-        if ((i & 1) && (i >> 1) + 2 < D / 16) qv[(i >> 1) & 1] = qfrag(sQw, f, (i >> 1) + 2);
 #pragma unroll
         for (int u = 0; u < PE; u += 2) {
           const int x = PE * i + u;
@@ -1112,9 +1115,8 @@ struct Prefill {
       // Upper half: PV of the last tile.
       if (lag) block_pv(sV + vb_cur * TILE_BYTES);
     }
-    // Every wave is past its last read of the K/V buffers: they are free for the staging.
-    __syncthreads();
-    epilogue(a, it, b, O, l_run, sKV + wave * WAVE_BYTES, lane);
+    // O is staged in the wave's own Q slot (Q is in registers): no other wave touches it.
+    epilogue(a, it, b, O, l_run, sQw, lane);
   }
 
   // Item index -> (qt, r, hs, b).  Per lane: v may differ between lanes (the startup reads two
@@ -1223,9 +1225,10 @@ struct Prefill {
         }
       }
     }
+    __syncthreads();  // publishes the row cache of item 0
     for (int i = 0;; ++i) {
-      // Publishes the metadata of item i and frees the K/V buffers (O staging of item i - 1).
-      __syncthreads();
+      // The metadata of item i was published by item i - 1's barriers; the K/V buffers are
+      // freed by the barrier in the item's prologue.
       // Values read from LDS are the same in every lane; readfirstlane lets the compiler keep
       // them (and the addresses derived from them) in scalar registers.
       const int v = __builtin_amdgcn_readfirstlane(s_vid[i & 3]);
