@@ -100,6 +100,17 @@ struct PrefillArgs {
 constexpr int MAX_ORDERED_ROWS = 256;
 __shared__ int s_row_rank[MAX_ORDERED_ROWS];
 
+// Sum / max of a value over lanes l and l ^ 32, in every lane: one v_permlane32_swap of the
+// value with itself puts the lower half's values in one result and the upper half's in the other.
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+}
+__device__ __forceinline__ float halves_max(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+}
+
 // floor(n / d) for n < 2^32 and 1 <= d < 2^32, given m = floor((2^32 - 1) / d): m >= (2^32 - d)/d,
 // so the high word of n*m is floor(n/d) or one less, and one compare corrects it.
 __device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t d, uint32_t m) {
@@ -551,7 +562,7 @@ struct Prefill {
                                                   const f32x16 (&O)[D / 32], float l_run, char* stage, int lane) {
     constexpr int NCH = D / 8;         // 16-byte chunks per row
     constexpr int RPI = 1024 / (2 * D);  // rows per 1 KiB wave-wide read
-    const float lt = l_run + swap_halves(l_run);
+    const float lt = halves_sum(l_run);
     const float inv = lt > 0.f ? 1.f / lt : 1.f;
 #pragma unroll
     for (int dt = 0; dt < D / 32; ++dt)
@@ -600,7 +611,7 @@ struct Prefill {
     float mx = S[0];
 #pragma unroll
     for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, S[rr]);
-    mx = fmaxf(mx, swap_halves(mx));
+    mx = halves_max(mx);
     const float m_tile = mx * c;  // -inf stays -inf (c > 0)
     float m = m_ref == -__builtin_inff() ? m_tile : m_ref;
     if (__any(m_tile > m + RESCALE_LOG2)) {
@@ -750,7 +761,7 @@ struct Prefill {
     for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, S[0][rr]);
 #pragma unroll
     for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, S[1][rr]);
-    mx = fmaxf(mx, swap_halves(mx));
+    mx = halves_max(mx);
     return mx * c;  // -inf stays -inf (c > 0)
   }
 
@@ -779,18 +790,19 @@ struct Prefill {
   struct Look {
     int e0, n_ent;        // this item's CSR entries
     int v1, e0_1, n_1;    // next item (>= n_items: none) and its CSR entries
+    int r_1;              // CSR row of the next item
     int v2;               // the item after it
     int n_items;
     int32_t* row_dst;     // row cache of the next item (and its sub-block masks)
     int32_t* mask_dst;
-    int* off_dst;         // CSR offsets (first, end) of item v2
-    int* vid_dst;         // slot of the newly claimed item
+    int* meta2;           // metadata slot of item v2: CSR offsets (first, end) and (qt, r, hs, b)
+    int* vid3;            // id slot of the newly claimed item
   };
   static constexpr int RPT = (RC + NT - 1) / NT;  // cached row entries per thread
   struct LookLoads {
     int32_t rv[RPT];
     int32_t mv[SUB ? RPT : 1];
-    int o0, o1;
+    int o0, o1, qt2, r2, hs2, b2;
     unsigned nv;
   };
 
@@ -805,11 +817,10 @@ struct Prefill {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int u = 0; u < RPT; ++u) ld.rv[u] = ld.mv[SUB ? u : 0] = 0;
-    ld.o0 = ld.o1 = 0;
+    ld.o0 = ld.o1 = ld.qt2 = ld.r2 = ld.hs2 = ld.b2 = 0;
     ld.nv = 0;
     if (lk.v1 < lk.n_items && lk.n_1 <= RC) {
-      int qt, r, hs, b;
-      decode_item_uniform(a, lk.v1, qt, r, hs, b);
+      const int r = lk.r_1;
       const int32_t* src = a.pairs + r * a.pairs_stride + lk.e0_1;
 #pragma unroll
       for (int u = 0; u < RPT; ++u)
@@ -823,7 +834,8 @@ struct Prefill {
     }
     if (tid == 0) {
       if (lk.v2 < lk.n_items) {
-        const int32_t* o = offsets_ptr(a, lk.v2);
+        decode_item(a, lk.v2, ld.qt2, ld.r2, ld.hs2, ld.b2);
+        const int32_t* o = a.offsets + ld.r2 * a.offsets_stride + (ld.qt2 >> a.qpb_log2);
         ld.o0 = o[0];
         ld.o1 = o[1];
       }
@@ -842,9 +854,13 @@ struct Prefill {
         }
     }
     if (tid == 0) {
-      lk.off_dst[0] = ld.o0;
-      lk.off_dst[1] = ld.o1;
-      lk.vid_dst[0] = (int)ld.nv;
+      lk.meta2[1] = ld.o0;
+      lk.meta2[2] = ld.o1;
+      lk.meta2[3] = ld.qt2;
+      lk.meta2[4] = ld.r2;
+      lk.meta2[5] = ld.hs2;
+      lk.meta2[6] = ld.b2;
+      lk.vid3[0] = (int)ld.nv;
     }
   }
 
@@ -972,7 +988,7 @@ struct Prefill {
         asm volatile("" : "+v"(mx));  // keeps the reduction spread over the MFMAs
         __builtin_amdgcn_sched_barrier(0);
       }
-      mx = fmaxf(mx, swap_halves(mx));
+      mx = halves_max(mx);
       return mx * c;
     };
 
@@ -1192,33 +1208,39 @@ struct Prefill {
   // first id past the end ends the loop in every wave at once.
   static __device__ __forceinline__ void run_lookahead(const PrefillArgs& a, int n_items, char* sKV, char* sQ,
                                                        int32_t* s_row, int32_t* s_mask) {
-    __shared__ int s_vid[4];
-    __shared__ int s_off[8];
+    // Per slot k = item index mod 4: id, CSR offsets (first, end) and (qt, r, hs, b); the loop
+    // top reads an item's whole slot (and the ids and offsets of the next two) in one batch.
+    __shared__ __attribute__((aligned(16))) int s_meta[4][8];
     const int tid = threadIdx.x;
     if (tid == 0) {
       const unsigned v0 = atomicAdd(&a.counter[0], 1u);
       const unsigned v1 = atomicAdd(&a.counter[0], 1u);
       const unsigned v2 = atomicAdd(&a.counter[0], 1u);
-      s_vid[0] = (int)v0;
-      s_vid[1] = (int)v1;
-      s_vid[2] = (int)v2;
+      s_meta[0][0] = (int)v0;
+      s_meta[1][0] = (int)v1;
+      s_meta[2][0] = (int)v2;
     }
     __syncthreads();
     if (tid < 2) {
-      const int v = s_vid[tid];
+      const int v = s_meta[tid][0];
       if (v < n_items) {
-        const int32_t* o = offsets_ptr(a, v);
-        s_off[2 * tid] = o[0];
-        s_off[2 * tid + 1] = o[1];
+        int qt, r, hs, b;
+        decode_item(a, v, qt, r, hs, b);
+        const int32_t* o = a.offsets + r * a.offsets_stride + (qt >> a.qpb_log2);
+        s_meta[tid][1] = o[0];
+        s_meta[tid][2] = o[1];
+        s_meta[tid][3] = qt;
+        s_meta[tid][4] = r;
+        s_meta[tid][5] = hs;
+        s_meta[tid][6] = b;
       }
     }
     __syncthreads();
     {
-      const int v = s_vid[0];
-      const int e0 = s_off[0], n = s_off[1] - e0;
+      const int v = s_meta[0][0];
+      const int e0 = s_meta[0][1], n = s_meta[0][2] - e0;
       if (v < n_items && n <= RC) {
-        int qt, r, hs, b;
-        decode_item_uniform(a, v, qt, r, hs, b);
+        const int r = __builtin_amdgcn_readfirstlane(s_meta[0][4]);
         for (int x = tid; x < n; x += NT) {
           s_row[x] = a.pairs[r * a.pairs_stride + e0 + x];
           if (SUB) s_mask[x] = a.tile_masks[r * a.masks_stride + e0 + x];
@@ -1228,25 +1250,34 @@ struct Prefill {
     __syncthreads();  // publishes the row cache of item 0
     for (int i = 0;; ++i) {
       // The metadata of item i was published by item i - 1's barriers; the K/V buffers are
-      // freed by the barrier in the item's prologue.
-      // Values read from LDS are the same in every lane; readfirstlane lets the compiler keep
-      // them (and the addresses derived from them) in scalar registers.
-      const int v = __builtin_amdgcn_readfirstlane(s_vid[i & 3]);
+      // freed by the barrier in the item's prologue.  Values read from LDS are the same in
+      // every lane; readfirstlane keeps them (and the addresses derived from them) in scalar
+      // registers.
+      const int k0 = i & 3, k1 = (i + 1) & 3, k2 = (i + 2) & 3;
+      const int4 m0 = *reinterpret_cast<const int4*>(&s_meta[k0][0]);  // id, first, end, qt
+      const int4 m0b = *reinterpret_cast<const int4*>(&s_meta[k0][4]);  // r, hs, b
+      const int4 m1 = *reinterpret_cast<const int4*>(&s_meta[k1][0]);
+      const int r1 = s_meta[k1][4];
+      const int v2 = s_meta[k2][0];
+      const int v = __builtin_amdgcn_readfirstlane(m0.x);
       if (v >= n_items) break;
       Look lk;
-      lk.e0 = __builtin_amdgcn_readfirstlane(s_off[2 * (i & 3)]);
-      lk.n_ent = __builtin_amdgcn_readfirstlane(s_off[2 * (i & 3) + 1]) - lk.e0;
-      lk.v1 = __builtin_amdgcn_readfirstlane(s_vid[(i + 1) & 3]);
-      lk.e0_1 = __builtin_amdgcn_readfirstlane(s_off[2 * ((i + 1) & 3)]);
-      lk.n_1 = __builtin_amdgcn_readfirstlane(s_off[2 * ((i + 1) & 3) + 1]) - lk.e0_1;
-      lk.v2 = __builtin_amdgcn_readfirstlane(s_vid[(i + 2) & 3]);
+      lk.e0 = __builtin_amdgcn_readfirstlane(m0.y);
+      lk.n_ent = __builtin_amdgcn_readfirstlane(m0.z) - lk.e0;
+      lk.v1 = __builtin_amdgcn_readfirstlane(m1.x);
+      lk.e0_1 = __builtin_amdgcn_readfirstlane(m1.y);
+      lk.n_1 = __builtin_amdgcn_readfirstlane(m1.z) - lk.e0_1;
+      lk.r_1 = __builtin_amdgcn_readfirstlane(r1);
+      lk.v2 = __builtin_amdgcn_readfirstlane(v2);
       lk.n_items = n_items;
       lk.row_dst = s_row + ((i + 1) & 1) * RC;
       lk.mask_dst = SUB ? s_mask + ((i + 1) & 1) * RC : s_mask;
-      lk.off_dst = s_off + 2 * ((i + 2) & 3);
-      lk.vid_dst = s_vid + ((i + 3) & 3);
-      int qt, r, hs, b;
-      decode_item_uniform(a, v, qt, r, hs, b);
+      lk.meta2 = &s_meta[k2][0];
+      lk.vid3 = &s_meta[(i + 3) & 3][0];
+      const int qt = __builtin_amdgcn_readfirstlane(m0.w);
+      const int r = __builtin_amdgcn_readfirstlane(m0b.x);
+      const int hs = __builtin_amdgcn_readfirstlane(m0b.y);
+      const int b = __builtin_amdgcn_readfirstlane(m0b.z);
       item_pipelined<true>(a, qt, r, hs, b, sKV, sQ, s_row + (i & 1) * RC, SUB ? s_mask + (i & 1) * RC : s_mask,
                            &lk);
     }
