@@ -784,9 +784,10 @@ struct Prefill {
 
   // ---- lookahead metadata (persistent four-head loop) -----------------------------------
   // While an item's first tiles load, the persistent loop fetches the CSR row of the next
-  // item, the CSR offsets of the item after it and a new claim from the counter.  All of it
-  // lands in LDS before the barrier that publishes the item's first tiles, so the next item
-  // starts without a dependent global read and no register stays live across the tile loop.
+  // item, the CSR offsets and decoded (qt, r, hs, b) of the item after it and a new claim
+  // from the counter.  All of it lands in LDS before the barrier that publishes the item's
+  // first tiles, so the next item starts without a dependent global read and no register
+  // stays live across the tile loop.
   struct Look {
     int e0, n_ent;        // this item's CSR entries
     int v1, e0_1, n_1;    // next item (>= n_items: none) and its CSR entries
@@ -805,13 +806,6 @@ struct Prefill {
     int o0, o1, qt2, r2, hs2, b2;
     unsigned nv;
   };
-
-  // Offsets entry of item v's query block in its CSR row.
-  static __device__ __forceinline__ const int32_t* offsets_ptr(const PrefillArgs& a, int v) {
-    int qt, r, hs, b;
-    decode_item(a, v, qt, r, hs, b);
-    return a.offsets + r * a.offsets_stride + (qt >> a.qpb_log2);
-  }
 
   static __device__ __forceinline__ void look_issue(const PrefillArgs& a, const Look& lk, LookLoads& ld) {
     const int tid = threadIdx.x;
@@ -867,10 +861,12 @@ struct Prefill {
   // Same work item as item(), with the tile loop software-pipelined: each step computes the
   // probabilities of tile i while the matrix cores already run S^T = K Q^T of tile i+1,
   // then O^T += V^T P^T of tile i while the VALU reduces the row max of tile i+1.
-  // Meanwhile the direct loads fetch K of tile i+2 (three K buffers) and V of tile i+1 (two
-  // V buffers).  Tiles that lie wholly after this wave's rows cost matrix work but add
-  // p == 0.  LOOK: the item's CSR row is already in s_row (lk->e0, lk->n_ent) and the
-  // lookahead reads of *lk run under the first tiles' loads.
+  // Meanwhile the direct loads fetch K of tile i+2 (two K buffers) and V of tile i+1 (three
+  // V buffers, for the upper half's lag).  Q goes through the wave's own LDS slot into
+  // registers once; the slot then stages O for the epilogue.  Tiles that lie wholly after
+  // this wave's rows cost matrix work but add p == 0.  LOOK: the item's CSR row is already
+  // in s_row (lk->e0, lk->n_ent) and the lookahead reads of *lk run under the first tiles'
+  // loads.
   template <bool LOOK>
   static __device__ __forceinline__ void item_pipelined(const PrefillArgs& a, int qt, int r, int hs, int b,
                                                         char* sKV, char* sQ, int32_t* s_row, int32_t* s_mask,
@@ -1201,11 +1197,12 @@ struct Prefill {
       item(a, qt, r, hs, b, sKV, s_row, s_mask);
   }
 
-  // Persistent four-head loop with lookahead.  Item i of this workgroup finds in LDS its id
-  // (s_vid[i % 4]), its CSR offsets (s_off[i % 4]) and row (row cache i % 2), and the id and
-  // offsets of item i + 1 and the id of item i + 2; its prologue fetches the row of item
-  // i + 1, the offsets of item i + 2 and claims item i + 3 (Look).  Claims only grow, so the
-  // first id past the end ends the loop in every wave at once.
+  // Persistent four-head loop with lookahead.  Item i of this workgroup finds in LDS its id,
+  // CSR offsets and (qt, r, hs, b) (slot i % 4 of s_meta) and its row (row cache i % 2), and
+  // the id, offsets and row of item i + 1 and the id of item i + 2; its prologue fetches the
+  // row of item i + 1, the offsets and (qt, r, hs, b) of item i + 2 and claims item i + 3
+  // (Look).  Claims only grow, so the first id past the end ends the loop in every wave at
+  // once.
   static __device__ __forceinline__ void run_lookahead(const PrefillArgs& a, int n_items, char* sKV, char* sQ,
                                                        int32_t* s_row, int32_t* s_mask) {
     // Per slot k = item index mod 4: id, CSR offsets (first, end) and (qt, r, hs, b); the loop
@@ -1308,8 +1305,7 @@ struct Prefill {
     }
 
     // Persistent: claim items from a counter until none is left.  The last workgroup to
-    // finish resets the counter pair to zero for the next launch on the stream.  The
-    // barriers also separate one item's epilogue (LDS staging) from the next item's loads.
+    // finish resets the counter pair to zero for the next launch on the stream.
     if (a.row_order) rank_rows(a, reinterpret_cast<int*>(sKV));  // K/V buffers are free here
     if constexpr (PIPE) {
       run_lookahead(a, n_items, sKV, sQ, s_row, s_mask);
