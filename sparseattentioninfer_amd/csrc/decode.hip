@@ -46,7 +46,7 @@ struct DecodeArgs {
 };
 
 constexpr int DEC_WAVES = 4;
-constexpr int DEC_NI = 8;        // 16-byte loads of K (and of V) per lane per round
+constexpr int DEC_NI = 4;        // 16-byte loads of K (and of V) per lane per round
 constexpr int DEC_CACHE = 512;   // retained blocks of a workgroup staged in LDS (longer lists read HBM)
 
 // x as held by the lane that DPP control CTRL selects (quad permutes, row mirrors: within 16 lanes).
@@ -66,12 +66,27 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
+// 32-bit global read that has completed when it returns: written as one opaque block, so the
+// compiler's count of outstanding loads (and its waits for the K/V rounds) never includes it.
+__device__ __forceinline__ int32_t load_now(const int32_t* p) {
+  int32_t x;
+  asm volatile(
+      "global_load_dword %0, %1, off\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=v"(x)
+      : "v"(p)
+      : "memory");
+  return x;
+}
+
 // Page of logical block lb of sequence b in a paged cache, or -1 where the block has no keys
 // below L, lies past the table's max_blocks columns, or maps outside the pool: such blocks load
-// nothing.
+// nothing.  NOW: read the table with load_now (inside the round loop).
+template <bool NOW = false>
 __device__ __forceinline__ int page_of(const DecodeArgs& a, int b, int lb, int L) {
   if (lb < 0 || lb >= a.max_blocks || (int64_t)lb * a.page >= L) return -1;
-  const int pg = a.block_table[b * a.bt_stride + lb];
+  const int32_t* t = a.block_table + b * a.bt_stride + lb;
+  const int pg = NOW ? load_now(t) : *t;
   return (pg >= 0 && pg < a.num_pages) ? pg : -1;
 }
 
@@ -92,23 +107,27 @@ struct Decode {
     const int32_t* s_blk;  // staged logical blocks (when cached)
     const int32_t* s_pg;   // staged pages (paged caches)
     const int32_t* selp;   // the global list (when not cached)
+    const elem_t* safe;    // 16 readable, finite bytes per lane (the query): loads of keys past nk
     int lo, b, kvh, L, rpb, kg, dc;
+    int n_it;              // rounds of the workgroup; rounds past it are dead (nk = 0)
     bool cached;
   };
 
   // Loads round `it` of the workgroup's list: keys k0 .. k0 + CH - 1 of retained entry it / rpb.
-  // Blocks past kv_len or with negative ids load nothing (nk = 0).
+  // Blocks past kv_len or with negative ids, and rounds past the list, have no keys (nk = 0).
   static __device__ __forceinline__ void issue(const DecodeArgs& a, const Ctx& c, int it, Round& R) {
     const int x = it / c.rpb;
     const int k0 = (it - x * c.rpb) * CH;
     int lb, pg = 0;
-    if (c.cached) {
+    if (it >= c.n_it) {
+      lb = -1;
+    } else if (c.cached) {
       lb = c.s_blk[x];
       pg = c.s_pg[x];
-    } else {
-      lb = c.selp[c.lo + x];
+    } else {  // lists longer than the LDS stage: entries read where they are used
+      lb = load_now(c.selp + c.lo + x);
       if (a.block_table) {
-        pg = page_of(a, c.b, lb, c.L);
+        pg = page_of<true>(a, c.b, lb, c.L);
         if (pg < 0) lb = -1;
       }
     }
@@ -127,12 +146,17 @@ struct Decode {
       kb = a.k + base;
       vb = a.v + base;
     }
+    // Every lane issues all its loads (lanes past nk read c.safe, and compute() masks their
+    // scores), so the compiler's wait before the round is computed covers exactly the loads
+    // issued before it and leaves the next round's loads in flight.
 #pragma unroll
     for (int i = 0; i < DEC_NI; ++i) {
       const int key = c.kg + KPI * i;
       const bool ok = key < nk;
-      R.k[i] = ok ? *reinterpret_cast<const u32x4*>(kb + key * a.kv_st + c.dc * 8) : u32x4{0, 0, 0, 0};
-      R.v[i] = ok ? *reinterpret_cast<const u32x4*>(vb + key * a.kv_st + c.dc * 8) : u32x4{0, 0, 0, 0};
+      const elem_t* pk = ok ? kb + key * a.kv_st + c.dc * 8 : c.safe;
+      const elem_t* pv = ok ? vb + key * a.kv_st + c.dc * 8 : c.safe;
+      R.k[i] = *reinterpret_cast<const u32x4*>(pk);
+      R.v[i] = *reinterpret_cast<const u32x4*>(pv);
     }
   }
 
@@ -218,6 +242,7 @@ struct Decode {
     c.dc = lane % LPR;  // head-dim chunk
     c.kg = lane / LPR;  // key row within a load instruction
     c.b = b;
+    c.safe = a.q + b * a.q_sb + h0 * a.q_sh + c.dc * 8;
     c.kvh = h0 / (a.Hq / a.Hkv);
     const int32_t* offp = a.sel_off + b * a.off_sb + r * a.off_sr;
     const int lo_all = offp[0];
@@ -264,16 +289,23 @@ struct Decode {
     // Rounds it = wave, wave + DEC_WAVES, ...: the next round's loads are issued before the
     // current round is computed (two register sets, alternating).
     const int n_items = nsel * c.rpb;
+    c.n_it = n_items;
+    // Every issue is unconditional (a round past the end is a dead one), so the loads form one
+    // straight sequence and the wait before a round's compute leaves the next round in flight.
     Round A, B;
     int it = wave;
-    if (it < n_items) issue(a, c, it, A);
+    // The fences keep each round's loads where they are written, ahead of the previous round's
+    // compute (the compiler would otherwise sink them below it).
+    issue(a, c, it, A);
     for (;;) {
       if (it >= n_items) break;
-      if (it + DEC_WAVES < n_items) issue(a, c, it + DEC_WAVES, B);
+      issue(a, c, it + DEC_WAVES, B);
+      asm volatile("" ::: "memory");
       compute(A, qp, a.scale_log2, c.kg, m_run, l_run, acc);
       it += DEC_WAVES;
       if (it >= n_items) break;
-      if (it + DEC_WAVES < n_items) issue(a, c, it + DEC_WAVES, A);
+      issue(a, c, it + DEC_WAVES, A);
+      asm volatile("" ::: "memory");
       compute(B, qp, a.scale_log2, c.kg, m_run, l_run, acc);
       it += DEC_WAVES;
     }
