@@ -240,8 +240,10 @@ def run_pattern_build(dev, reps: int = 20):
                      "the reference's Python build on its own (unstated) hardware")}
 
 
-def decode_workload(dev):
-    """paged bf16 cache, 64 sequences x 16384 tokens, BigBird-style block selection."""
+def decode_workload(dev, random_blocks: int = 8):
+    """paged bf16 cache, 64 sequences x 16384 tokens, BigBird-style block selection
+    (2 global + 4 local + ``random_blocks`` seeded random blocks per sequence and KV group: 8 is the
+    configuration's count, 14 blocks = 5.5 %; 16 gives the 8.6 % its description quotes)."""
     import torch
     from sparseattentioninfer_amd.patterns import decode_selection
     B, Hq, Hkv, D, page, L = 64, 32, 8, 128, 64, 16384
@@ -253,7 +255,7 @@ def decode_workload(dev):
     q = torch.randn(B, Hq, D, generator=g, device=dev).to(torch.bfloat16)
     table = torch.randperm(P, generator=torch.Generator().manual_seed(4049)).to(torch.int32).reshape(B, nblk)
     lens = torch.full((B,), L, dtype=torch.int32)
-    sel, sel_off = decode_selection(B, Hkv, nblk, local=4, global_blocks=2, random_blocks=8, seed=4050)
+    sel, sel_off = decode_selection(B, Hkv, nblk, local=4, global_blocks=2, random_blocks=random_blocks, seed=4050)
     kept = int(sel_off[:, :, 1].sum().item())           # (sequence, KV head, block) triples
     kv_bytes = kept * page * D * 2 * 2
     io_bytes = 2 * B * Hq * D * 2                        # q in, o out
@@ -283,9 +285,11 @@ def stream_read_ceiling(dev, nbytes: int = 4 << 30, reps: int = 20) -> dict:
     return {"gbs": nbytes / (ev / reps) / 1e9, "bytes": nbytes, "launches": reps}
 
 
-def run_decode(args, dev):
+def _time_decode(args, dev, random_blocks: int):
+    """Fastest of num_splits 1 and 2 (or the one asked for): (kernel s, wall s per step, splits,
+    workload info, bytes per launch)."""
     from sparseattentioninfer_amd import ops
-    (q, kp, vp, table, lens, sel, sel_off), info, nbytes = decode_workload(dev)
+    (q, kp, vp, table, lens, sel, sel_off), info, nbytes = decode_workload(dev, random_blocks)
     steps = max(10 * args.steps, 100)
     best = None
     for splits in ([args.decode_splits] if args.decode_splits else [1, 2]):
@@ -295,9 +299,22 @@ def run_decode(args, dev):
         cand = (ev / steps, wall / steps, splits)
         if best is None or cand[0] < best[0]:
             best = cand
-    avg, per_step, splits = best
+    del q, kp, vp
+    return (*best, info, nbytes, steps)
+
+
+def run_decode(args, dev):
+    avg, per_step, splits, info, nbytes, steps = _time_decode(args, dev, 8)
     gbs = nbytes / avg / 1e9
     info["num_splits"] = splits
+    # The same workload at 22 retained blocks per row (8.6 % of the cache), the retention the
+    # configuration's description quotes; reported beside the 14-block line, not as its value.
+    avg22, _, splits22, info22, nbytes22, _ = _time_decode(args, dev, 16)
+    info["at_22_blocks"] = {
+        "retained_blocks_per_row": info22["retained_blocks_per_row"],
+        "retained_fraction": info22["retained_fraction"], "num_splits": splits22,
+        "kernel_us": avg22 * 1e6, "bytes_per_launch": nbytes22, "gbs": nbytes22 / avg22 / 1e9,
+        "frac": nbytes22 / avg22 / 1e9 / PEAK_HBM_GBS}
     ceiling = stream_read_ceiling(dev)
     info["stream_read_ceiling_gbs"] = ceiling["gbs"]
     info["frac_of_stream_read"] = gbs / ceiling["gbs"]
@@ -426,6 +443,7 @@ def _attach_traffic(line: dict, prefill_first: bool) -> None:
         put(line["configs1"]["roofline"], "prefill_cfg1")
     if "decode" in line:
         put(line["decode"]["roofline"], "decode_cfg3")
+        put(line["decode"].get("at_22_blocks"), "decode_cfg3_22")
         if not prefill_first and "roofline" in line:
             put(line["roofline"], "decode_cfg3")
 
