@@ -461,7 +461,8 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); multi-GPU runs are not part of "
-              "this build (see DESIGN.md: how the path would shard).", file=sys.stderr)
+              "this build: prefill would shard by KV group and decode by sequence, with no exchange "
+              "on either path.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
