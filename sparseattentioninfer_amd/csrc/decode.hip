@@ -109,6 +109,7 @@ struct Decode {
     const int32_t* selp;   // the global list (when not cached)
     const elem_t* safe;    // 16 readable, finite bytes per lane (the query): loads of keys past nk
     int lo, b, kvh, L, rpb, kg, dc;
+    uint32_t nb;           // blocks holding keys below L: ids at or past it (or negative) have none
     int n_it;              // rounds of the workgroup; rounds past it are dead (nk = 0)
     bool cached;
   };
@@ -133,7 +134,8 @@ struct Decode {
     }
     lb = __builtin_amdgcn_readfirstlane(lb);
     pg = __builtin_amdgcn_readfirstlane(pg);
-    const int nk = lb < 0 ? 0 : max(0, min(min(CH, a.page - k0), c.L - lb * a.page - k0));
+    // one unsigned test for negative ids and ids at or past the last block (no lb * page overflow)
+    const int nk = (uint32_t)lb >= c.nb ? 0 : max(0, min(min(CH, a.page - k0), c.L - lb * a.page - k0));
     R.nk = nk;
     const elem_t* kb;
     const elem_t* vb;
@@ -252,6 +254,7 @@ struct Decode {
     c.selp = a.sel + b * a.sel_sb + r * a.sel_sr;
     c.L = a.kv_lens ? a.kv_lens[b] : a.kv_len;
     c.rpb = (a.page + CH - 1) / CH;  // rounds per block
+    c.nb = (uint32_t)(((int64_t)max(c.L, 0) + a.page - 1) / a.page);
     const int nsel = hi - c.lo;
     c.cached = nsel <= DEC_CACHE;
     c.s_blk = s_blk;

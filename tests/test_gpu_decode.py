@@ -1,4 +1,5 @@
 """GPU parity of the HIP decode kernel (paged and contiguous) against the oracle."""
+import math
 import sys
 
 import numpy as np
@@ -113,3 +114,92 @@ def test_configs_3_full_size_every_sequence(random_blocks):
         max_abs, mean_abs = assert_close_bf16(out, want, f"configs[3] {6 + random_blocks} blocks splits={splits}")
         _say(f"[decode] configs[3] {6 + random_blocks} blocks splits={splits}: all 64 sequences, "
              f"max-abs {max_abs:.3e}, mean-abs {mean_abs:.3e}")
+
+
+def _with_skipped_entries(valid: list[int], junk: list[int], seed: int) -> list[int]:
+    """``valid`` with each entry of ``junk`` inserted at a seeded position."""
+    g = torch.Generator().manual_seed(seed)
+    out = list(valid)
+    for x in junk:
+        out.insert(int(torch.randint(0, len(out) + 1, (1,), generator=g)), x)
+    return out
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3])
+def test_paged_lists_longer_than_the_lds_stage(splits):
+    """Rows of 1,000+ retained blocks (page 16, 16384 keys): longer than the 512 entries a
+    workgroup stages in LDS, so num_splits 1 and 2 read the list and the block table where they
+    are used and 3 stages them.  Mixed in are entries the kernel skips: -1 and -7, ids past kv_len,
+    past the table's columns, 2^30, and block 7, whose page lies outside the pool.  The third
+    sequence is empty (kv_len 0, output 0).  Expected: the oracle over the valid entries only."""
+    _say(f"[decode] long lists, splits={splits}")
+    B, Hq, Hkv, D, page = 3, 8, 2, 128, 16
+    lens = [16384, 9000, 0]
+    nblk = [-(-L // page) for L in lens]
+    max_blocks = max(nblk)
+    P = sum(nblk) + 2
+    kp = seeded((P, Hkv, page, D), 41, torch.bfloat16)
+    vp = seeded((P, Hkv, page, D), 42, torch.bfloat16)
+    q = seeded((B, Hq, D), 43, torch.bfloat16)
+    perm = torch.randperm(P, generator=torch.Generator().manual_seed(44)).to(torch.int32)
+    table = torch.zeros(B, max_blocks, dtype=torch.int32)
+    used = 0
+    for b, n in enumerate(nblk):
+        table[b, :n] = perm[used:used + n]
+        used += n
+    table[0, 7] = P + 100
+    table[1, 7] = -5
+    lists, clean = [], []
+    for b in range(B):
+        for r in range(Hkv):
+            valid = list(range(nblk[b]))
+            junk = [-1, nblk[b], nblk[b] + 3, max_blocks + 9, 1 << 30, -7]
+            lists.append(_with_skipped_entries(valid, junk, seed=100 * b + r))
+            clean.append([x for x in valid if x != 7])
+    assert max(len(x) for x in lists) // splits > 512 or splits == 3
+
+    def pack(rows):
+        width = max(1, max(len(x) for x in rows))
+        sel = torch.zeros(B, Hkv, width, dtype=torch.int32)
+        off = torch.zeros(B, Hkv, 2, dtype=torch.int32)
+        for i, x in enumerate(rows):
+            sel[i // Hkv, i % Hkv, :len(x)] = torch.tensor(x, dtype=torch.int32)
+            off[i // Hkv, i % Hkv, 1] = len(x)
+        return sel, off
+
+    sel, sel_off = pack(lists)
+    csel, csel_off = pack(clean)
+    kv_lens = torch.tensor(lens, dtype=torch.int32)
+    out = ops.paged_sparse_decode(q.to(DEV), kp.to(DEV), vp.to(DEV), table.to(DEV), kv_lens.to(DEV),
+                                  sel.to(DEV), sel_off.to(DEV), num_splits=splits)
+    torch.cuda.synchronize()
+    want = oa.paged_decode_attention(q, kp.to(DEV), vp.to(DEV), table.numpy(), kv_lens.numpy(),
+                                     csel.numpy(), csel_off.numpy(), device=DEV)
+    assert torch.isfinite(out.float()).all()
+    assert (out[2].float() == 0).all()
+    max_abs, _ = assert_close_bf16(out, want, f"long lists splits={splits}")
+    _say(f"[decode] long lists, splits={splits}: max-abs {max_abs:.3e}")
+
+
+def test_contiguous_lists_longer_than_the_lds_stage():
+    """A contiguous cache (the backend's T_q == 1 path) with every one of 1,024 blocks of 16 keys
+    retained, in a list longer than the LDS stage, plus entries it skips: -1, -2, the block at T_k,
+    2^30 and 2^31 - 1 (whose key offset does not fit 32 bits).  Expected: attention over all keys,
+    which is what a full decode row is (fp32 torch reference)."""
+    _say("[decode] contiguous long list")
+    B, Hq, Hkv, D, bs, T = 2, 8, 2, 128, 16, 16384
+    q = seeded((B, Hq, 1, D), 51, torch.bfloat16).to(DEV)
+    k = seeded((B, Hkv, T, D), 52, torch.bfloat16).to(DEV)
+    v = seeded((B, Hkv, T, D), 53, torch.bfloat16).to(DEV)
+    lst = _with_skipped_entries(list(range(T // bs)), [-1, T // bs, 1 << 30, (1 << 31) - 1, -2], seed=54)
+    pairs = torch.tensor([lst] * Hkv, dtype=torch.int32, device=DEV)
+    offsets = torch.tensor([[0, len(lst)]] * Hkv, dtype=torch.int32, device=DEV)
+    out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs)
+    torch.cuda.synchronize()
+    kf = k.float().repeat_interleave(Hq // Hkv, dim=1)
+    vf = v.float().repeat_interleave(Hq // Hkv, dim=1)
+    s = (q.float() @ kf.transpose(-1, -2).contiguous()) / math.sqrt(D)
+    want = torch.softmax(s, dim=-1) @ vf
+    assert torch.isfinite(out.float()).all()
+    max_abs, _ = assert_close_bf16(out, want, "contiguous long list")
+    _say(f"[decode] contiguous long list: max-abs {max_abs:.3e}")
