@@ -423,11 +423,21 @@ struct Prefill {
     return it.qb + (int64_t)row * a.q_st + 8 * it.g;
   }
 
-  static __device__ __forceinline__ int tile_of(const PrefillArgs& a, const Item& it, const int32_t* s_row, int t) {
+  // Last key tile an item can use: it starts before T_k and at or before the causal limit of the
+  // whole query tile (-1: none).
+  static __device__ __forceinline__ int kt_limit(const PrefillArgs& a, const Item& it) {
+    return it.q_abs_tile_max < 0 ? -1 : min((a.Tk + KT - 1) / KT - 1, it.q_abs_tile_max / KT);
+  }
+
+  // Key tile of schedule position t, or -1 for a negative block id or one past kt_hi's block
+  // (rejected before the shift, which cannot overflow then).
+  static __device__ __forceinline__ int tile_of(const PrefillArgs& a, const Item& it, const int32_t* s_row, int t,
+                                                int kt_hi) {
     const int e = t >> a.tpb_log2;
     // Two distinct loads (LDS cache, or a global read past the cached entries), so the two are
     // not merged into one flat load of a selected pointer.
     const int blk = it.cached ? s_row[e] : load_uniform_now(it.prow + it.e0 + e);
+    if (blk < 0 || blk > (kt_hi >> a.tpb_log2)) return -1;
     return (blk << a.tpb_log2) + (t & it.tpb_mask);
   }
 
@@ -460,14 +470,14 @@ struct Prefill {
     return ((bits >> sh) & 1u) ? lim : -1;
   }
 
-  // First tile at or after t that can contribute: tiles entirely past T_k or above the
-  // causal limit of the whole 64-row query tile are skipped, and so are negative ids
-  // (malformed schedules) rather than read.
+  // First tile at or after t that can contribute (0 <= kt <= kt_hi = kt_limit()): tiles entirely
+  // past T_k or above the causal limit of the whole 64-row query tile are skipped, and so are
+  // negative ids (malformed schedules) rather than read.
   static __device__ __forceinline__ int next_usable(const PrefillArgs& a, const Item& it, const int32_t* s_row,
-                                                    int t) {
+                                                    int t, int kt_hi) {
     for (; t < it.n_tiles; ++t) {
-      const int kt = tile_of(a, it, s_row, t);
-      if (kt >= 0 && kt * KT < a.Tk && kt * KT <= it.q_abs_tile_max) break;
+      const int kt = tile_of(a, it, s_row, t, kt_hi);
+      if (kt >= 0 && kt <= kt_hi) break;
     }
     return t;
   }
@@ -491,7 +501,7 @@ struct Prefill {
     q.m = 0;
     q.live = 0;
     q.next = 0;
-    q.kt_hi = min((a.Tk + KT - 1) / KT - 1, it.q_abs_tile_max / KT);
+    q.kt_hi = min((a.Tk + KT - 1) / KT - 1, it.q_abs_tile_max / KT);  // kt_limit() for q_abs_tile_max >= 0
     return q;
   }
 
@@ -689,10 +699,11 @@ struct Prefill {
     float l_run = 0.f;  // this lane's half of the row sum
     const float c = a.scale_log2;
 
-    int t = next_usable(a, it, s_row, 0);
+    const int kt_hi = kt_limit(a, it);
+    int t = next_usable(a, it, s_row, 0, kt_hi);
     int buf = 0;
     if (t < it.n_tiles) {
-      const int kt = tile_of(a, it, s_row, t);
+      const int kt = tile_of(a, it, s_row, t, kt_hi);
       dma<true>(it.kb, a.k_st, dl.k, sK, kt, a.Tk, wave, lane);
       dma<false>(it.vb, a.v_st, dl.v, sV, kt, a.Tk, wave, lane);
     }
@@ -700,10 +711,10 @@ struct Prefill {
     __syncthreads();
 
     while (t < it.n_tiles) {
-      const int kt = tile_of(a, it, s_row, t);
-      const int tn = next_usable(a, it, s_row, t + 1);
+      const int kt = tile_of(a, it, s_row, t, kt_hi);
+      const int tn = next_usable(a, it, s_row, t + 1, kt_hi);
       if (NBK == 2 && tn < it.n_tiles) {
-        const int ktn = tile_of(a, it, s_row, tn);
+        const int ktn = tile_of(a, it, s_row, tn, kt_hi);
         dma<true>(it.kb, a.k_st, dl.k, sK + (buf ^ 1) * TILE_BYTES, ktn, a.Tk, wave, lane);
         dma<false>(it.vb, a.v_st, dl.v, sV + (buf ^ 1) * TILE_BYTES, ktn, a.Tk, wave, lane);
       }
@@ -724,7 +735,7 @@ struct Prefill {
 
       if (NBK == 1 && tn < it.n_tiles) {
         __syncthreads();  // single buffer: every wave is done reading it
-        const int ktn = tile_of(a, it, s_row, tn);
+        const int ktn = tile_of(a, it, s_row, tn, kt_hi);
         dma<true>(it.kb, a.k_st, dl.k, sK, ktn, a.Tk, wave, lane);
         dma<false>(it.vb, a.v_st, dl.v, sV, ktn, a.Tk, wave, lane);
       }

@@ -261,18 +261,21 @@ def _csr(rows):
     return pairs, offsets
 
 
-@pytest.mark.parametrize("bs", [64, 128])
-def test_long_rows_with_unusable_entries(bs):
-    """Four-head (pipelined) workgroups over rows of hundreds to over a thousand entries: schedule
-    positions are read 64 at a time, rows past the 1,024-entry LDS cache from global memory, and
-    entries the kernel skips fall anywhere in a row, including on 64-position boundaries.  Blocks
-    wholly after the query tile's causal limit are checked against the oracle (which masks them);
-    blocks past T_k and negative ids, which the oracle cannot take, must leave the bits of the
+@pytest.mark.parametrize("bs,Hq", [(64, 4), (128, 4), (64, 1), (128, 2)],
+                         ids=["bs64_4heads", "bs128_4heads", "bs64_1head", "bs128_2heads"])
+def test_long_rows_with_unusable_entries(bs, Hq):
+    """Rows of hundreds to over a thousand entries, shared by 4 query heads (the pipelined
+    four-head workgroups, which read schedule positions 64 at a time), by 2 or by 1 (the one- and
+    two-head workgroups, which walk the row entry by entry); rows past the 1,024-entry LDS cache
+    are read from global memory, and entries the kernel skips fall anywhere in a row, including on
+    64-position boundaries.  Blocks wholly after the query tile's causal limit are checked against
+    the oracle (which masks them); blocks past T_k, negative ids and ids whose key offset does not
+    fit 32 bits (2^25, 2^30, 2^31 - 1), which the oracle cannot take, must leave the bits of the
     result unchanged."""
-    B, Hq, Hkv, D = 1, 4, 1, 128
+    B, Hkv, D = 1, 1, 128
     T_q, T_k = 2 * bs, (70000 if bs == 64 else 40000)
     nkb, nqb = -(-T_k // bs), 2
-    _say(f"[prefill] long rows bs={bs} T_k={T_k}")
+    _say(f"[prefill] long rows bs={bs} Hq={Hq} T_k={T_k}")
     rng = np.random.default_rng(bs)
     clean, junk = [], []
     for qb in range(nqb):
@@ -283,7 +286,8 @@ def test_long_rows_with_unusable_entries(bs):
         else:
             blocks = sorted(rng.choice(nkb, size=min(600, nkb // 2), replace=False).tolist())
         bad = list(blocks)
-        for pos, blk in ((0, -1), (63, nkb), (64, -1), (65, nkb + 3), (127, -2), (300, nkb + 1), (len(bad), -1)):
+        for pos, blk in ((0, -1), (63, nkb), (64, -1), (65, nkb + 3), (127, -2), (200, 1 << 30),
+                         (201, (1 << 31) - 1), (202, 1 << 25), (300, nkb + 1), (len(bad), -1)):
             bad.insert(min(pos, len(bad)), blk)
         clean.append(blocks)
         junk.append(bad)
@@ -296,4 +300,4 @@ def test_long_rows_with_unusable_entries(bs):
     torch.cuda.synchronize()
     assert torch.equal(out, out_j), "skipped entries changed the result"
     want = oa.block_sparse_attention(q, k, v, pairs, offsets, bs)
-    assert_close_bf16(out, want, f"long rows bs={bs}")
+    assert_close_bf16(out, want, f"long rows bs={bs} Hq={Hq}")
