@@ -150,15 +150,18 @@ struct Decode {
     }
     // Every lane issues all its loads (lanes past nk read c.safe, and compute() masks their
     // scores), so the compiler's wait before the round is computed covers exactly the loads
-    // issued before it and leaves the next round's loads in flight.
+    // issued before it and leaves the next round's loads in flight.  The loads are
+    // non-temporal: K/V are read once per step, and reads that do not allocate in the Infinity
+    // Cache leave more of HBM's bandwidth to the stream (a cache-cold step: 42.4 against 47.7 us
+    // at 236 MB per launch).
 #pragma unroll
     for (int i = 0; i < DEC_NI; ++i) {
       const int key = c.kg + KPI * i;
       const bool ok = key < nk;
       const elem_t* pk = ok ? kb + key * a.kv_st + c.dc * 8 : c.safe;
       const elem_t* pv = ok ? vb + key * a.kv_st + c.dc * 8 : c.safe;
-      R.k[i] = *reinterpret_cast<const u32x4*>(pk);
-      R.v[i] = *reinterpret_cast<const u32x4*>(pv);
+      R.k[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pk));
+      R.v[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(pv));
     }
   }
 
