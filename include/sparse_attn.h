@@ -262,9 +262,10 @@ int64_t sa_decode_noalloc_scratch_bytes(void);
 
 /*
  * Measurement aid, no counterpart in the reference: reads `bytes` (a multiple
- * of 16) at src once with 16-byte loads from sa_stream_read_workgroups()
- * workgroups (8 per CU) and writes one xor-folded word per workgroup to sink
- * (that many uint32).  Its rate is the HBM streaming-read ceiling that the
+ * of 16) at src once with 16-byte non-temporal loads from
+ * sa_stream_read_workgroups() workgroups (8 per CU), each reading one
+ * contiguous chunk, and writes one xor-folded word per workgroup to sink (that
+ * many uint32).  Its rate is the HBM streaming-read ceiling that the
  * memory-bound decode kernel is compared with.
  */
 int sa_stream_read(const void* src, int64_t bytes, uint32_t* sink, void* stream);
