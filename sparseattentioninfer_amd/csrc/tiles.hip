@@ -67,10 +67,14 @@ __device__ __forceinline__ bool merge_tiles(const TileArgs& a, const int32_t* pr
     ascending &= kt > last;
     last = kt;
     uint32_t m = 0;
+    // Negative ids between a tile's entries are skipped here too: tested only as id / s == kt, an
+    // id in (-s, 0) would pass for kt = 0 (division truncates toward zero) and set a wrong bit.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-      while (pos[i] < end[i] && prow[pos[i]] / s == kt) {
-        m |= 1u << (i * s + prow[pos[i]] % s);
+      while (pos[i] < end[i]) {
+        const int id = prow[pos[i]];
+        if (id >= 0 && id / s != kt) break;
+        if (id >= 0) m |= 1u << (i * s + id % s);
         ++pos[i];
       }
     emit(kt, m);

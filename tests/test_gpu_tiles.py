@@ -90,6 +90,20 @@ def test_csr_to_tiles_drops_negative_ids_and_handles_empty_rows():
                                               1 << (12 + 3)]
 
 
+@pytest.mark.parametrize("bs", [16, 32])
+def test_csr_to_tiles_negative_ids_after_tile_zero_entries(bs):
+    """Negative ids inside a query block's list, right after entries of key tile 0: an id in (-s, 0)
+    divided by s truncates to 0, the tile being collected, and must still be dropped rather than set
+    a sub-block bit (regression: it set bit i*s - 1, a pair of another query sub-block)."""
+    _say(f"[tiles] negative ids after tile 0, bs={bs}")
+    s = 64 // bs
+    # query blocks 0..3, ascending ids once the negatives are dropped: {0, 1}, {s-1, s}, {0}, {1, s, 2s+1}
+    pairs = torch.tensor([[0, -1, 1, s - 1, -(s - 1), s, -1, 0, -1, -1, 1, -2, s, -1, 2 * s + 1, -3]],
+                         dtype=torch.int32)
+    offsets = torch.tensor([[0, 3, 6, 9, 16]], dtype=torch.int32)
+    _check_tiles(pairs, offsets, bs)
+
+
 def _mask(kind, rows, T_q, T_k, bs, seed):
     nqb, nkb = -(-T_q // bs), -(-T_k // bs)
     qbo = (T_k - T_q) // bs
