@@ -3,7 +3,8 @@ block sizes, chunked query offsets, ragged cache lengths, page sizes, split coun
 per case.  Each prefill case also runs on a copy of its CSR with entries the kernel skips (negative
 ids anywhere, ids past T_k at the end of a query block's list) and must give the same bits; each
 decode case mixes such entries into its lists and is checked against the oracle over the valid
-entries only."""
+entries only.  The backend cases build the reference-compatible pattern classes at random shapes
+and run them through ``HipBlockSparseBackend.forward``."""
 import sys
 
 import numpy as np
@@ -164,3 +165,68 @@ def test_random_prefill_case(seed):
 @pytest.mark.parametrize("seed", range(24))
 def test_random_decode_case(seed):
     run_decode_case(seed)
+
+
+def backend_case(seed: int):
+    """A reference-compatible pattern class at a random shape, prefill, decode or chunked."""
+    from sparseattentioninfer_amd import patterns as P
+    rng = np.random.default_rng(9000 + seed)
+    Hkv = int(rng.integers(1, 5))
+    Hq = Hkv * int(rng.choice([1, 2, 4]))
+    B = int(rng.integers(1, 3))
+    D = int(rng.choice([64, 128]))
+    T_k = int(rng.integers(16, 3000))
+    mode = str(rng.choice(["prefill", "decode", "chunk"]))
+    T_q = T_k if mode == "prefill" else (1 if mode == "decode" else int(rng.integers(2, T_k + 1)))
+    kind = str(rng.choice(["bigbird", "bigbird2", "keep", "keep_groups", "local", "dense", "seeded", "bernoulli"]))
+    dtype = torch.bfloat16 if rng.random() < 0.7 else torch.float16
+    bs = int(rng.choice([16, 32, 64, 128]))
+    if kind == "bigbird":
+        pat = P.BigBirdPattern(top_k=int(rng.choice([16, 32, 64, 128, 256])), n_heads=Hq)
+    elif kind == "bigbird2":
+        pat = P.BigBird2Pattern(top_k=int(rng.choice([16, 32, 64, 128])), n_heads=Hq)
+    elif kind == "keep":
+        pat = P.BigBirdKeepRatioPattern(keep_ratio=float(rng.choice([0.1, 0.25, 0.5])), n_heads=Hq)
+    elif kind == "keep_groups":
+        pat = P.BigBirdKeepRatioPattern(group_sparsities=[float(x) for x in rng.choice([0.5, 0.7, 0.9], size=Hkv)],
+                                        n_heads=Hq, n_kv_heads=Hkv)
+    elif kind == "local":
+        pat = P.LocalWindowPattern(window_size=int(rng.integers(8, 700)), block_size=bs)
+    elif kind == "dense":
+        pat = P.DenseCausalPattern()
+    elif kind == "seeded":
+        pat = P.SeededBigBirdPattern(rows=Hkv, block_size=bs, seed=seed)
+    else:
+        pat = P.BernoulliBlockPattern(rows=Hkv, density=float(rng.choice([0.05, 0.3])), block_size=bs, seed=seed)
+    return dict(pat=pat, kind=kind, mode=mode, B=B, Hq=Hq, Hkv=Hkv, D=D, T_q=T_q, T_k=T_k, dtype=dtype)
+
+
+def run_backend_case(seed: int):
+    from sparseattentioninfer_amd.attention import get_backend
+    c = backend_case(seed)
+    tag = (f"seed {seed}: {c['kind']} {c['mode']} B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} D={c['D']} "
+           f"T_q={c['T_q']} T_k={c['T_k']} {str(c['dtype'])[6:]}")
+    _say(f"[random backend] {tag}")
+    Hq, Hkv, D, T_q, T_k = c["Hq"], c["Hkv"], c["D"], c["T_q"], c["T_k"]
+    q = seeded((c["B"], Hq, T_q, D), seed, c["dtype"]).to(DEV)
+    k = seeded((c["B"], Hkv, T_k, D), seed + 1, c["dtype"]).to(DEV)
+    v = seeded((c["B"], Hkv, T_k, D), seed + 2, c["dtype"]).to(DEV)
+    meta = c["pat"].build(q, k, causal=True)
+    be = get_backend("hip_block_sparse")
+    out = be.forward(q, k, v, meta)
+    torch.cuda.synchronize()
+    assert be.actual_backend == "hip_block_sparse" and torch.isfinite(out.float()).all(), tag
+    if meta.kind == "dense":   # bottom-right causal over all keys, fp32
+        kf, vf = oa.repeat_kv(k.float(), Hq // Hkv), oa.repeat_kv(v.float(), Hq // Hkv)
+        s = (q.float() @ kf.transpose(-1, -2).contiguous()) / D ** 0.5
+        keep = torch.arange(T_k, device=DEV)[None, :] <= (T_k - T_q) + torch.arange(T_q, device=DEV)[:, None]
+        want = torch.softmax(s.masked_fill(~keep, float("-inf")), dim=-1) @ vf
+    else:                      # the kernels' semantics on the pattern's own CSR
+        want = oa.block_sparse_attention(q, k, v, meta.block_pairs.cpu(), meta.block_pair_offsets.cpu(),
+                                         meta.block_size)
+    return assert_close_bf16(out, want, tag)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_backend_case(seed):
+    run_backend_case(seed)
