@@ -66,6 +66,22 @@ __device__ __forceinline__ float row_sum(float x) {
   return x;
 }
 
+// Max (MAX) or sum of x over the lanes that differ from this one only in lane bits log2(LPR)..5,
+// i.e. over the key rows of a round, in every lane and without an LDS round trip: xor 8 by a DPP
+// row rotation (LPR 8), then xor 16 and xor 32 by v_permlane16_swap / v_permlane32_swap of the
+// value with itself, whose two results hold the values of the two lanes.  The steps and the pairs
+// they combine are those of __shfl_xor by 8, 16, 32, so the results are the same bits.
+template <int LPR, bool MAX>
+__device__ __forceinline__ float over_rows(float x) {
+  static_assert(LPR == 8 || LPR == 16, "key rows span 8 or 16 lanes");
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if constexpr (LPR == 8) x = op(x, dpp_get<0x128>(x));  // row_ror:8: lane i <-> i ^ 8 within its row
+  const auto s16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = op(__uint_as_float(s16[0]), __uint_as_float(s16[1]));
+  const auto s32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return op(__uint_as_float(s32[0]), __uint_as_float(s32[1]));
+}
+
 // 32-bit global read that has completed when it returns: written as one opaque block, so the
 // compiler's count of outstanding loads (and its waits for the K/V rounds) never includes it.
 __device__ __forceinline__ int32_t load_now(const int32_t* p) {
@@ -191,8 +207,7 @@ struct Decode {
         sc[i][h] = x;
         mx = fmaxf(mx, x);
       }
-#pragma unroll
-      for (int msk = LPR; msk < 64; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+      mx = over_rows<LPR, true>(mx);
       const float m_new = fmaxf(m_run[h], mx);
       const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
       const float alpha = fast_exp2(m_run[h] - m_use);
@@ -318,13 +333,11 @@ struct Decode {
 
     // merge the key rows of the wave (lanes with equal dc), then the waves through LDS
 #pragma unroll
-    for (int msk = LPR; msk < 64; msk <<= 1)
+    for (int h = 0; h < NH; ++h) {
+      l_run[h] = over_rows<LPR, false>(l_run[h]);
 #pragma unroll
-      for (int h = 0; h < NH; ++h) {
-        l_run[h] += __shfl_xor(l_run[h], msk, 64);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[h][e] += __shfl_xor(acc[h][e], msk, 64);
-      }
+      for (int e = 0; e < 8; ++e) acc[h][e] = over_rows<LPR, false>(acc[h][e]);
+    }
     // every lane of a row group holds the same sums; lanes 0..LPR-1 publish them
     if (c.kg == 0) {
 #pragma unroll
