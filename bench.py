@@ -16,9 +16,18 @@ group), same units.  (``decode``): the paged sparse decode of configs[3] (B=64
 sequences, 16384 cached tokens each in 64-token pages, 14 retained blocks per
 (sequence, KV head)) in tokens/s and HBM GB/s, timed cache-cold (independent
 workloads launched in turn, so K/V come from HBM rather than the Infinity
-Cache; one workload repeated is reported beside it); and ``cpu_baseline``: the
+Cache; one workload repeated is reported beside it); ``attn_launch_tok_per_s``
+there is the 64 sequences of one attention launch divided by its time, not a
+model's decode rate (that is ``e2e.decode_tok_per_s``).  ``cpu_baseline``: the
 dense-masked PyTorch path (the reference's ``MaskedSdpaBackend`` arithmetic,
-restated in ``oracle/``) on the host cores, on a bounded sample of configs[2].
+restated in ``oracle/``) on the host cores, on a bounded sample of configs[2];
+each other block carries its own ``cpu_baseline`` (configs[1] rows, configs[3]
+decode rows, one configs[4] decoder layer), timed in the same run.
+
+Timing discipline: every kernel leg first launches back to back for about 0.25 s
+(``settle_launches`` at the top level of the line and in each block) so the
+power controller has settled, then runs ``warmup`` untimed and ``steps`` timed
+launches.
 
 ``e2e`` (skip with ``--no-e2e``) is configs[4]: a random-init Qwen3-4B-architecture decoder (36
 layers, BigBird window 3 / global 2 / random 3 in layers 0-17, dense causal
@@ -155,7 +164,20 @@ def prefill_workload(dev, copies: int = 1):
         "group_density": [round(x / causal_blocks, 4) for x in nnz_group.tolist()],
     }
     flops = info["retained_pairs"] * PAIR_FLOP * D
+    info["flops_exact_causal"] = exact_causal_flops(bm, Hq // Hkv, D)
     return (sets, pairs.to(dev), offsets.to(dev), bm), info, flops
+
+
+def exact_causal_flops(bm, heads_per_row: int, D: int, batch: int = 1) -> int:
+    """FLOP of the (query, key) pairs the causal mask leaves visible in the retained blocks: a
+    block below the diagonal holds 64 * 64 of them, a diagonal block 64 * 65 / 2 (its upper
+    triangle removed); 4 * D FLOP each (QK^T and PV)."""
+    import torch
+    nqb, nkb = bm.shape[1], bm.shape[2]
+    diag = torch.diagonal(bm, dim1=1, dim2=2).sum().item()
+    below = bm.sum().item() - diag
+    visible = below * BS * BS + diag * BS * (BS + 1) // 2
+    return int(visible) * heads_per_row * batch * 4 * D
 
 
 def run_prefill(args, dev):
@@ -173,14 +195,20 @@ def run_prefill(args, dev):
     info = {**info, "timing": f"{PREFILL_ROTATION} independent q/k/v sets launched in turn",
             "kernel_us_one_set_repeated": round(ev_one / args.steps * 1e6, 2),
             "settle_launches": settle, "kernel_us_before_settle": round(ev_cold / args.steps * 1e6, 2)}
+    exact = info["flops_exact_causal"]
     res = {
         "value": flops / (wall / args.steps) / 1e12,
         "ms_per_step": wall / args.steps * 1e3,
         "kernel_us": avg * 1e6,
         "flops_per_launch": flops,
+        "settle_launches": settle,
         "info": info,
         "roofline": {"bound": "mfma", "achieved": flops / avg / 1e12, "peak": PEAK_BF16_TFLOPS,
-                     "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None},
+                     "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None,
+                     "exact_causal": {"flops_per_launch": exact, "achieved": exact / avg / 1e12,
+                                      "frac": exact / avg / 1e12 / PEAK_BF16_TFLOPS,
+                                      "note": "secondary count: retained blocks with the masked upper triangle "
+                                              "of each diagonal block removed"}},
         "tensors": (q, k, v, bm),
     }
     return res
@@ -214,24 +242,27 @@ def bernoulli_workload(dev, copies: int = 1):
         "group_density": [round(x / causal_blocks, 4) for x in nnz_group.tolist()],
     }
     flops = info["retained_pairs"] * PAIR_FLOP * D
-    return (sets, pairs.to(dev), offsets.to(dev)), info, flops
+    info["flops_exact_causal"] = exact_causal_flops(bm, Hq // Hkv, D, B)
+    return (sets, pairs.to(dev), offsets.to(dev), bm), info, flops
 
 
 def run_prefill_bernoulli(args, dev):
     from sparseattentioninfer_amd import ops
-    (sets, pairs, offsets), info, flops = bernoulli_workload(dev, PREFILL_ROTATION)
+    (sets, pairs, offsets, bm), info, flops = bernoulli_workload(dev, PREFILL_ROTATION)
     launches = [ops.prepare_prefill(q, k, v, pairs, offsets, BS) for (q, k, v) in sets]
     launch = _rotation(launches)
     settle = _settle(launch)
     wall, ev = _events_time(launch, args.steps, args.warmup)
     _, ev_one = _events_time(launches[0], args.steps, args.warmup)
     avg = ev / args.steps
+    q, k, v = sets[0]
     return {**info, "timing": f"{PREFILL_ROTATION} independent q/k/v sets launched in turn",
             "kernel_us_one_set_repeated": round(ev_one / args.steps * 1e6, 2),
             "steps": args.steps, "warmup": args.warmup, "settle_launches": settle, "ms_per_step": wall / args.steps * 1e3,
             "kernel_us": avg * 1e6, "tflops": flops / (wall / args.steps) / 1e12, "flops_per_launch": flops,
             "roofline": {"bound": "mfma", "achieved": flops / avg / 1e12, "peak": PEAK_BF16_TFLOPS,
-                         "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None}}
+                         "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None},
+            "tensors": (q, k, v, bm)}
 
 
 def run_pattern_build(dev, reps: int = 20):
@@ -343,19 +374,20 @@ def _time_decode(args, dev, random_blocks: int):
     for splits in ([args.decode_splits] if args.decode_splits else [1, 2]):
         launches = [ops.prepare_paged_decode(*w, num_splits=splits) for w in work]
         rotate = _rotation(launches)
-        _settle(rotate)
+        settle = _settle(rotate)
         wall, ev = _events_time(rotate, steps, max(args.warmup, 10))
         _, ev_warm = _events_time(launches[0], steps, max(args.warmup, 10))
-        cand = (ev / steps, wall / steps, splits, ev_warm / steps)
+        cand = (ev / steps, wall / steps, splits, ev_warm / steps, settle)
         if best is None or cand[0] < best[0]:
             best = cand
         del launches, rotate
+    first = work[0]
     del work
-    return (*best, info, nbytes, steps)
+    return (*best, info, nbytes, steps, first)
 
 
 def run_decode(args, dev):
-    avg, per_step, splits, warm, info, nbytes, steps = _time_decode(args, dev, 8)
+    avg, per_step, splits, warm, settle, info, nbytes, steps, work0 = _time_decode(args, dev, 8)
     gbs = nbytes / avg / 1e9
     info["num_splits"] = splits
     info["timing"] = (f"cache-cold: {DECODE_ROTATION} workloads (own page tables and selections over one pool, "
@@ -363,7 +395,7 @@ def run_decode(args, dev):
     info["kernel_us_one_workload_repeated"] = warm * 1e6
     # The same workload at 22 retained blocks per row (8.6 % of the cache), the retention the
     # configuration's description quotes; reported beside the 14-block line, not as its value.
-    avg22, _, splits22, warm22, info22, nbytes22, _ = _time_decode(args, dev, 16)
+    avg22, _, splits22, warm22, _, info22, nbytes22, _, _ = _time_decode(args, dev, 16)
     info["at_22_blocks"] = {
         "retained_blocks_per_row": info22["retained_blocks_per_row"],
         "retained_fraction": info22["retained_fraction"], "num_splits": splits22,
@@ -376,51 +408,168 @@ def run_decode(args, dev):
     return {
         **info,
         "steps": steps,
+        "settle_launches": settle,
         "us_per_step": per_step * 1e6,
         "kernel_us": avg * 1e6,
-        "tok_per_s": info["batch"] / per_step,
+        # one token for each of the batch's sequences per attention launch (one layer), not a
+        # model's decode rate
+        "attn_launch_tok_per_s": info["batch"] / per_step,
         "bytes_per_launch": nbytes,
         "roofline": {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": gbs / PEAK_HBM_GBS, "traffic": None},
+        "workload0": work0,
     }
 
 
-def cpu_baseline(prefill_res, budget_s):
+def _host_cores() -> str:
+    import torch
+    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    return f"host os.cpu_count()={os.cpu_count()}, affinity={aff}, torch threads={torch.get_num_threads()}"
+
+
+def cpu_baseline(prefill_res, budget_s, which: str = "configs[2]"):
     """Dense-masked fp32 attention (oracle restatement of masked_sdpa.py:23-68) on host cores,
-    over sampled (query head, query block) rows of configs[2]; effective TFLOP/s on the same
-    retained-block numerator as the GPU figure."""
+    over sampled (batch, query head, query block) rows of a prefill workload; effective TFLOP/s
+    on the same retained-block numerator as the GPU figure."""
     import numpy as np
     import torch
     from oracle.attention import masked_sdpa_rows
     q, k, v, bm = prefill_res["tensors"]
-    Hq, T, D = q.shape[1], q.shape[2], q.shape[3]
+    B, Hq, T, D = q.shape
     Hkv = k.shape[1]
     n_rep = Hq // Hkv
-    kc = k[0].float().cpu()
-    vc = v[0].float().cpu()
     rng = np.random.default_rng(0)
     nqb = T // BS
+    cache = {}
     flops = 0
     n = 0
     elapsed = 0.0
     while elapsed < budget_s or n < 4:
-        h, qb = int(rng.integers(Hq)), int(rng.integers(nqb))
+        b, h, qb = int(rng.integers(B)), int(rng.integers(Hq)), int(rng.integers(nqb))
         g = h // n_rep
-        qr = q[0, h, qb * BS:(qb + 1) * BS].float().cpu()
-        blk = bm[g, qb]                                              # [NKB] retained key blocks
+        if (b, g) not in cache:
+            if len(cache) >= 4:                                      # bound host memory
+                cache.pop(next(iter(cache)))
+            cache[(b, g)] = (k[b, g].float().cpu(), v[b, g].float().cpu())
+        kc, vc = cache[(b, g)]
+        qr = q[b, h, qb * BS:(qb + 1) * BS].float().cpu()
+        blk = bm[g, qb].cpu()                                        # [NKB] retained key blocks
         keep = blk.repeat_interleave(BS)[None, :T].expand(BS, T)
         keep = keep & (torch.arange(T)[None, :] <= (qb * BS + torch.arange(BS))[:, None])
         t0 = time.perf_counter()
-        masked_sdpa_rows(qr, kc[g], vc[g], keep)
+        masked_sdpa_rows(qr, kc, vc, keep)
         elapsed += time.perf_counter() - t0
         flops += int(blk.sum().item()) * PAIR_FLOP * D
         n += 1
-    aff = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     return {"value": flops / elapsed / 1e12, "unit": "TFLOP/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": (f"{n} (query head, query block) rows of configs[2] drawn uniformly (seed 0); each row "
+            "sample": (f"{n} (batch, query head, query block) rows of {which} drawn uniformly (seed 0); each row "
                        f"dense-masked fp32 over all {T} keys as masked_sdpa.py does; {elapsed:.1f} s of CPU "
-                       f"time; host os.cpu_count()={os.cpu_count()}, affinity={aff}")}
+                       f"time; {_host_cores()}")}
+
+
+def cpu_decode_baseline(decode_res, budget_s):
+    """The decode row of the dense-masked path (masked_sdpa.py:42-46: one query per sequence
+    against the whole cache, K/V repeated to the query heads, -inf outside the retained blocks),
+    fp32 on the host cores, over sampled sequences of configs[3]; sequences (tokens) per second
+    and GB/s on the same algorithmic-bytes numerator as the GPU figure."""
+    import torch
+    from oracle.attention import masked_sdpa
+    q, kp, vp, table, lens, sel, sel_off = decode_res["workload0"]
+    B, Hq, D = q.shape
+    Hkv, page = kp.shape[1], kp.shape[2]
+    n_rep = Hq // Hkv
+    per_seq_bytes = decode_res["bytes_per_launch"] / B
+    SAMPLED = 2        # sequences gathered to the host (about 0.5 GB each once repeated to 32 heads)
+    inputs = []
+    for b in range(min(SAMPLED, B)):
+        L = int(lens[b].item())
+        nblk = -(-L // page)
+        pages = table[b, :nblk].long()
+        k = kp[pages].permute(1, 0, 2, 3).reshape(Hkv, nblk * page, D)[:, :L].float().cpu()
+        v = vp[pages].permute(1, 0, 2, 3).reshape(Hkv, nblk * page, D)[:, :L].float().cpu()
+        keep = torch.zeros(Hq, 1, L, dtype=torch.bool)
+        for g in range(Hkv):
+            lo, hi = sel_off[b, g].tolist()
+            for blk in sel[b, g, lo:hi].tolist():
+                keep[g * n_rep:(g + 1) * n_rep, 0, blk * page:min(L, (blk + 1) * page)] = True
+        inputs.append((q[b].float().cpu()[None, :, None], k.repeat_interleave(n_rep, dim=0)[None],
+                       v.repeat_interleave(n_rep, dim=0)[None], keep))
+    n, elapsed = 0, 0.0
+    while elapsed < budget_s or n < 2:
+        qb, kr, vr, keep = inputs[n % len(inputs)]
+        t0 = time.perf_counter()
+        masked_sdpa(qb, kr, vr, "mask", keep)
+        elapsed += time.perf_counter() - t0
+        n += 1
+    del inputs
+    return {"value": n / elapsed, "unit": "tok/s", "gbs": n * per_seq_bytes / elapsed / 1e9,
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"{n} decode rows over {min(SAMPLED, B)} sequences of configs[3] (one token each, all {Hq} "
+                       "query heads, the sequences taken in turn) through the "
+                       f"dense-masked fp32 decode row over the whole {int(lens[0].item())}-token cache, K/V "
+                       f"repeated to the query heads as the reference's callers do; {elapsed:.1f} s of CPU time; "
+                       f"gbs counts the retained K/V bytes the GPU figure counts; {_host_cores()}")}
+
+
+class _CpuMaskedSdpa:
+    """The reference's MaskedSdpaBackend arithmetic (restated in ``oracle/``), injected as the
+    kernel backend's fallback: what a CPU fp32 run of the reference's Qwen3 layer executes."""
+
+    def forward(self, q, k, v, pattern):
+        import torch
+        from oracle import attention as oa
+        from oracle import csr as ocsr
+        nkb = -(-k.size(2) // pattern.block_size)
+        bm = ocsr.csr_to_block_mask(pattern.block_pairs.cpu().numpy(), pattern.block_pair_offsets.cpu().numpy(), nkb)
+        return oa.masked_sdpa_blockwise(q, k, v, torch.from_numpy(bm), pattern.block_size).to(q.dtype)
+
+
+def cpu_e2e_layer_baseline():
+    """One sparse decoder layer of configs[4] (layer 0: BigBird window 3 / global 2 / random 3,
+    block 64) on the host cores in fp32, as the reference's Qwen3 integration runs it on a CPU: the
+    kernel backend falls back to the dense-masked path.  Times the layer over one 8192-token
+    prompt sequence, then one decode token against that cache."""
+    import warnings
+
+    import torch
+    from transformers.cache_utils import DynamicCache
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3DecoderLayer, Qwen3RotaryEmbedding
+    from sparseattentioninfer_amd.qwen3 import build_sparse_attention_from_dense
+    from sparseattentioninfer_amd.qwen3.runtime import qwen3_config
+    cfg = qwen3_config(sparse_layers=range(18), pattern="seeded_bigbird", block_size=BS, window=3,
+                       global_blocks=2, random_blocks=3, seed=11)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    layer = Qwen3DecoderLayer(cfg, 0).float().eval()
+    with torch.no_grad():
+        for prm in layer.parameters():
+            if prm.dim() == 2:
+                prm.normal_(0.0, cfg.initializer_range)
+    layer.self_attn = build_sparse_attention_from_dense(layer.self_attn, backend_name="hip_block_sparse",
+                                                        block_size=BS, fallback=_CpuMaskedSdpa)
+    rope = Qwen3RotaryEmbedding(cfg)
+    T = 8192
+    x = torch.randn(1, T, cfg.hidden_size, generator=torch.Generator().manual_seed(1)) * 0.5
+    cache = DynamicCache(config=cfg)
+    with torch.no_grad(), warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        pos = torch.arange(T)[None]
+        t0 = time.perf_counter()
+        layer(x, position_embeddings=rope(x, pos), past_key_values=cache, use_cache=True)
+        prompt_s = time.perf_counter() - t0
+        xt = x[:, -1:]
+        pos1 = torch.tensor([[T]])
+        t0 = time.perf_counter()
+        layer(xt, position_embeddings=rope(xt, pos1), past_key_values=cache, use_cache=True)
+        decode_s = time.perf_counter() - t0
+    actual = layer.self_attn.sparse_backend.actual_backend
+    return {"prompt_layer_s": prompt_s, "decode_layer_s": decode_s, "unit": "s", "cores": torch.get_num_threads(),
+            "kind": "port", "actual_backend": actual,
+            "sample": (f"one decoder layer (layer 0, BigBird) of configs[4] in fp32 for ONE sequence: an {T}-token "
+                       "prompt forward, then one decode token against its cache; attention core dense-masked as "
+                       f"the reference's CPU fallback runs it (actual_backend {actual}); {_host_cores()}. The GPU "
+                       "figures beside it are for the whole 36-layer model and 8 sequences")}
 
 
 def run_e2e(args, dev):
@@ -553,11 +702,19 @@ def main():
         line["ms_per_step"] = round(pre["ms_per_step"], 4)
         line["config"] = {**pre["info"], "kernel_us": round(pre["kernel_us"], 2),
                           "flops_per_launch": pre["flops_per_launch"]}
+        line["settle_launches"] = pre["settle_launches"]
         line["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre["roofline"].items()}
+        ex = line["roofline"]["exact_causal"]
+        line["roofline"]["exact_causal"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in ex.items()}
     if args.only in ("all", "bernoulli"):
         c1 = run_prefill_bernoulli(args, dev)
         c1["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c1["roofline"].items()}
-        line["configs1"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c1.items()}
+        line["configs1"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c1.items() if k != "tensors"}
+        if not args.no_cpu_baseline and args.only == "all":
+            cb1 = cpu_baseline(c1, args.cpu_seconds / 3, "configs[1]")
+            cb1["value"] = round(cb1["value"], 5)
+            line["configs1"]["cpu_baseline"] = cb1
+        del c1
         if pre is None and args.only == "bernoulli":
             line.update(value=round(c1["tflops"], 3), ms_per_step=round(c1["ms_per_step"], 4),
                         config={"workload": c1["workload"], "kernel_us": round(c1["kernel_us"], 2)},
@@ -565,15 +722,27 @@ def main():
     if args.only in ("all", "decode"):
         dec = run_decode(args, dev)
         dec["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()}
-        line["decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in dec.items()}
+        line["decode"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in dec.items() if k != "workload0"}
+        if not args.no_cpu_baseline and args.only == "all":
+            cbd = cpu_decode_baseline(dec, args.cpu_seconds / 3)
+            line["decode"]["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cbd.items()}
+        del dec
         if pre is None:
-            line.update(value=round(dec["tok_per_s"], 1), unit="tok/s", ms_per_step=round(dec["us_per_step"] / 1e3, 4),
-                        config={"workload": dec["workload"]}, roofline=line["decode"]["roofline"])
+            line.update(value=round(line["decode"]["attn_launch_tok_per_s"], 1), unit="tok/s",
+                        ms_per_step=round(line["decode"]["us_per_step"] / 1e3, 4),
+                        config={"workload": line["decode"]["workload"]}, roofline=line["decode"]["roofline"])
     if args.only == "all":
         pb = run_pattern_build(dev)
         line["pattern_build"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pb.items()}
     if e2e_done is not None:
         line["e2e"] = e2e_done
+        if not args.no_cpu_baseline and "error" not in e2e_done:
+            try:
+                cbl = cpu_e2e_layer_baseline()
+                line["e2e"]["cpu_baseline_one_layer"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                                         for k, v in cbl.items()}
+            except Exception as exc:
+                line["e2e"]["cpu_baseline_one_layer"] = {"error": f"{type(exc).__name__}: {exc}"}
     if pre is not None and not args.no_cpu_baseline:
         cb = cpu_baseline(pre, args.cpu_seconds)
         cb["value"] = round(cb["value"], 5)

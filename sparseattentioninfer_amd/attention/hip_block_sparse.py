@@ -142,11 +142,14 @@ class HipBlockSparseBackend(AttentionBackend):
     @staticmethod
     def unsupported_reason(q: torch.Tensor, pattern: PatternMetadata):
         """Why the kernels cannot take these inputs (the reference backends' fallback conditions,
-        ``triton_universal_backend.py:54-61``, plus top-k patterns), or None when they can."""
+        ``triton_universal_backend.py:54-61``, plus head dims other than 64 and 128 and top-k
+        patterns), or None when they can."""
         if not q.is_cuda:
             return "a CPU tensor"
         if q.dtype not in (torch.float16, torch.bfloat16):
             return f"dtype {q.dtype} (the kernels take float16 and bfloat16)"
+        if q.size(-1) not in (64, 128):
+            return f"head dim {q.size(-1)} (the kernels take 64 and 128)"
         if pattern.kind in ("mask", "local"):
             if pattern.block_size is None:
                 return "pattern.block_size is None"

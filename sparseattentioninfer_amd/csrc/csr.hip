@@ -180,8 +180,13 @@ extern "C" int sa_block_mask_to_csr(const uint8_t* mask, int64_t mask_row_stride
     return set_error(SA_E_SHAPE, "sa_block_mask_to_csr: bad sizes rows=%d nqb=%d nkb=%d", rows, nqb, nkb);
   if (pairs && (width < 1 || !status))
     return set_error(SA_E_SHAPE, "sa_block_mask_to_csr: the write pass needs width >= 1 and a status word");
-  if ((int64_t)nqb * nkb > 0x7fffffff || (int64_t)rows * nqb > ((int64_t)1 << 40))
+  if ((int64_t)nqb * nkb > 0x7fffffff)
     return set_error(SA_E_SHAPE, "sa_block_mask_to_csr: %d x %d blocks per row is too many", nqb, nkb);
+  // One wave per (row, query block) in one launch, whose grid holds fewer than 2^32 threads.
+  constexpr int64_t max_waves = ((int64_t)0xffffffff / CSR_THREADS) * CSR_WAVES;
+  if ((int64_t)rows * nqb > max_waves)
+    return set_error(SA_E_SHAPE, "sa_block_mask_to_csr: %d rows x %d query blocks is more than the %lld one launch covers",
+                     rows, nqb, (long long)max_waves);
   if (rows == 0) return 0;
   if (!offsets || !nnz || (nqb && nkb && !mask)) return set_error(SA_E_NULL, "sa_block_mask_to_csr: NULL pointer");
   CsrArgs a;

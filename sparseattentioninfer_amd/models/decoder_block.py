@@ -1,23 +1,24 @@
 """Toy decoder for the layer and decoder benchmarks.
 
-Drop-in for the constructors of ``sparse_attentions/models/decoder_block.py:49-125``:
-``DecoderBlock(d_model, num_heads, pattern, backend, mlp_ratio=4, causal=True)`` and
-``ToyDecoder(vocab_size, d_model, num_heads, num_layers, pattern, backend, max_seq_len=4096,
-mlp_ratio=4, causal=True)`` with ``forward(x, kv_cache=None, layer_idx=0)`` and
-``forward(input_ids, kv_cache=None, pos_offset=0)``.  The computation is the same pre-norm
-decoder (RMSNorm with eps 1e-6, GELU feed-forward of width ``mlp_ratio * d_model``, learned
-absolute positions, output head tied to the token embedding); the module structure is this
-build's own:
+Drop-in for ``sparse_attentions/models/decoder_block.py:18-125``: the classes ``RMSNorm``, ``MLP``,
+``DecoderBlock`` and ``ToyDecoder`` with the reference's constructors,
+``DecoderBlock.forward(x, kv_cache=None, layer_idx=0)`` and
+``ToyDecoder.forward(input_ids, kv_cache=None, pos_offset=0)``.
 
-* a block is two :class:`PreNormResidual` sublayers, ``x + body(rms_norm(x))``, one around the
-  attention layer and one around the feed-forward ``nn.Sequential``;
-* norms call ``torch.nn.functional.rms_norm`` with a learned scale;
-* the output head is ``F.linear(h, embedding.weight)``, so the tie needs no second module;
-* ``pattern`` and ``backend`` may also be sequences with one entry per layer (e.g. sparse
-  attention in the first layers only), and ``num_kv_heads`` gives grouped-query attention.
+The submodule names are part of the interface, not a choice made here: the reference's decoder
+runner reads ``model.blocks[0].attn.backend.actual_backend``
+(``sparse_attention_bench/runners/decoder_sweep_runner.py:116``) and copies weights between a
+dense and a sparse decoder with ``load_state_dict``, so a checkpoint's keys (``token_emb``,
+``pos_emb``, ``blocks.<i>.norm1 / attn / norm2 / mlp.fc1 / mlp.fc2``, ``norm_f``, ``lm_head``)
+must mean the same thing here.  The computation is the same pre-norm decoder (RMSNorm with eps
+1e-6, exact-GELU feed-forward of width ``mlp_ratio * d_model``, learned absolute positions,
+output head tied to the token embedding).  Beyond the reference:
 
-State dicts round-trip between two ``ToyDecoder`` instances of equal shape, which is how the
-benchmarks give a sparse and a dense model the same weights.
+* ``pattern`` and ``backend`` may be sequences with one entry per layer (sparse attention in the
+  first layers only, say), and ``num_kv_heads`` gives grouped-query attention;
+* norms run ``torch.nn.functional.rms_norm`` (one fused kernel) instead of a chain of
+  elementwise operations;
+* positions past ``max_seq_len`` raise ``ValueError`` with the offending range.
 """
 from __future__ import annotations
 
@@ -32,46 +33,47 @@ from ..patterns.base import SparsePattern
 from .attention_layer import AttentionLayer
 from .kv_cache import KVCache
 
-NORM_EPS = 1e-6
 
+class RMSNorm(nn.Module):
+    """``x / sqrt(mean(x^2) + eps) * weight`` over the last dimension; parameter ``weight``."""
 
-class PreNormResidual(nn.Module):
-    """``x + body(rms_norm(x) * scale)``; keyword arguments of the call go to ``body``."""
-
-    def __init__(self, dim: int, body: nn.Module, eps: float = NORM_EPS):
+    def __init__(self, dim: int, eps: float = 1e-6):
         super().__init__()
-        self.scale = nn.Parameter(torch.ones(dim))
         self.eps = eps
-        self.body = body
+        self.weight = nn.Parameter(torch.ones(dim))
 
-    def forward(self, x: torch.Tensor, **body_kwargs) -> torch.Tensor:
-        h = F.rms_norm(x, (x.size(-1),), self.scale, self.eps)
-        return x + self.body(h, **body_kwargs)
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return F.rms_norm(x, self.weight.shape, self.weight, self.eps)
 
 
-def feed_forward(d_model: int, mlp_ratio: int) -> nn.Sequential:
-    """``d_model -> mlp_ratio * d_model -> d_model`` with an exact GELU, no biases."""
-    width = d_model * mlp_ratio
-    return nn.Sequential(nn.Linear(d_model, width, bias=False), nn.GELU(), nn.Linear(width, d_model, bias=False))
+class MLP(nn.Module):
+    """``fc2(gelu(fc1(x)))`` with hidden width ``mlp_ratio * d_model``."""
+
+    def __init__(self, d_model: int, mlp_ratio: int = 4, bias: bool = False):
+        super().__init__()
+        self.fc1 = nn.Linear(d_model, mlp_ratio * d_model, bias=bias)
+        self.act = nn.GELU()
+        self.fc2 = nn.Linear(mlp_ratio * d_model, d_model, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.fc2(self.act(self.fc1(x)))
 
 
 class DecoderBlock(nn.Module):
-    """Pre-norm attention sublayer followed by a pre-norm feed-forward sublayer."""
+    """``x + attn(norm1(x))``, then ``x + mlp(norm2(x))``."""
 
     def __init__(self, d_model: int, num_heads: int, pattern: SparsePattern, backend: AttentionBackend,
                  mlp_ratio: int = 4, causal: bool = True, *, num_kv_heads: int | None = None):
         super().__init__()
-        attn = AttentionLayer(d_model=d_model, num_heads=num_heads, pattern=pattern, backend=backend,
-                              causal=causal, num_kv_heads=num_kv_heads)
-        self.attention = PreNormResidual(d_model, attn)
-        self.ffn = PreNormResidual(d_model, feed_forward(d_model, mlp_ratio))
-
-    @property
-    def attn(self) -> AttentionLayer:
-        return self.attention.body
+        self.norm1 = RMSNorm(d_model)
+        self.attn = AttentionLayer(d_model=d_model, num_heads=num_heads, pattern=pattern, backend=backend,
+                                   causal=causal, num_kv_heads=num_kv_heads)
+        self.norm2 = RMSNorm(d_model)
+        self.mlp = MLP(d_model, mlp_ratio)
 
     def forward(self, x: torch.Tensor, kv_cache: KVCache | None = None, layer_idx: int = 0) -> torch.Tensor:
-        return self.ffn(self.attention(x, kv_cache=kv_cache, layer_idx=layer_idx))
+        h = x + self.attn(self.norm1(x), kv_cache=kv_cache, layer_idx=layer_idx)
+        return h + self.mlp(self.norm2(h))
 
 
 def _per_layer(value, n: int, what: str) -> list:
@@ -93,21 +95,21 @@ class ToyDecoder(nn.Module):
                  num_kv_heads: int | None = None):
         super().__init__()
         self.max_seq_len = max_seq_len
-        self.embedding = nn.Embedding(vocab_size, d_model)
-        self.positions = nn.Parameter(torch.randn(max_seq_len, d_model))
-        patterns = _per_layer(pattern, num_layers, "pattern")
-        backends = _per_layer(backend, num_layers, "backend")
-        self.layers = nn.ModuleList(
+        self.token_emb = nn.Embedding(vocab_size, d_model)
+        self.pos_emb = nn.Embedding(max_seq_len, d_model)
+        per_layer = zip(_per_layer(pattern, num_layers, "pattern"), _per_layer(backend, num_layers, "backend"))
+        self.blocks = nn.ModuleList(
             DecoderBlock(d_model, num_heads, p, be, mlp_ratio=mlp_ratio, causal=causal, num_kv_heads=num_kv_heads)
-            for p, be in zip(patterns, backends))
-        self.final_scale = nn.Parameter(torch.ones(d_model))
+            for p, be in per_layer)
+        self.norm_f = RMSNorm(d_model)
+        self.lm_head = nn.Linear(d_model, vocab_size, bias=False)
+        self.lm_head.weight = self.token_emb.weight  # tied: one parameter under both keys
 
     def forward(self, input_ids: torch.Tensor, kv_cache: KVCache | None = None, pos_offset: int = 0) -> torch.Tensor:
         T = input_ids.size(1)
-        if pos_offset + T > self.max_seq_len:
-            raise ValueError(f"positions {pos_offset}..{pos_offset + T - 1} exceed max_seq_len {self.max_seq_len}")
-        h = self.embedding(input_ids) + self.positions[pos_offset:pos_offset + T]
-        for idx, layer in enumerate(self.layers):
-            h = layer(h, kv_cache=kv_cache, layer_idx=idx)
-        h = F.rms_norm(h, (h.size(-1),), self.final_scale, NORM_EPS)
-        return F.linear(h, self.embedding.weight)
+        if pos_offset < 0 or pos_offset + T > self.max_seq_len:
+            raise ValueError(f"positions {pos_offset}..{pos_offset + T - 1} outside max_seq_len {self.max_seq_len}")
+        h = self.token_emb(input_ids) + self.pos_emb.weight[pos_offset:pos_offset + T]
+        for idx, blk in enumerate(self.blocks):
+            h = blk(h, kv_cache=kv_cache, layer_idx=idx)
+        return self.lm_head(self.norm_f(h))

@@ -72,6 +72,33 @@ class GroupSparsitySpec:
         return GroupSparsitySpec(other.default if other.default is not None else self.default,
                                  other.per_layer if other.per_layer is not None else self.per_layer)
 
+    @classmethod
+    def with_config_defaults(cls, config, default=None, per_layer=None) -> "GroupSparsitySpec":
+        """The arguments, each validated, with the config's value standing in for an argument that
+        is None; a config value is validated only when it is used, as the reference's
+        ``replace_qwen3_attention_with_sparse`` does (``modeling_sparse_qwen3.py:358-376``)."""
+        spec = cls.build(default, per_layer)
+        if spec.default is None:
+            spec = cls(_as_sparsities(config_value(config, "sparse_attention_group_sparsities", None),
+                                      "config.sparse_attention_group_sparsities"), spec.per_layer)
+        if spec.per_layer is None:
+            spec = cls(spec.default, cls.build(None, config_value(config, "sparse_attention_layer_group_sparsities",
+                                                                   None),
+                                               where="config.sparse_attention_group_sparsities").per_layer)
+        return spec
+
+    @staticmethod
+    def resolve_layer(config, layer_idx: int) -> Optional[Sparsities]:
+        """A layer's sparsities from the config alone: its per-layer entry (the whole per-layer list is
+        validated), else the model-wide default, validated only when it is the one used
+        (``modeling_sparse_qwen3.py:123-141``)."""
+        layers = GroupSparsitySpec.build(None, config_value(config, "sparse_attention_layer_group_sparsities", None),
+                                         where="config.sparse_attention_group_sparsities").per_layer
+        if layers is not None and layer_idx < len(layers) and layers[layer_idx] is not None:
+            return layers[layer_idx]
+        return _as_sparsities(config_value(config, "sparse_attention_group_sparsities", None),
+                              "config.sparse_attention_group_sparsities")
+
     def for_layer(self, layer_idx: int) -> Optional[Sparsities]:
         if self.per_layer is not None and layer_idx < len(self.per_layer) \
                 and self.per_layer[layer_idx] is not None:

@@ -64,6 +64,9 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     assert st == -2 and b"width >= 1" in lib.sa_last_error()
     st = lib.sa_block_mask_to_csr(None, 0, 0, 2, 4, 4, None, 0, None, None, 0, 0, None, None)
     assert st == -6
+    # one wave per (row, query block) in one launch: past 2^32 grid threads it is refused, not truncated
+    st = lib.sa_block_mask_to_csr(None, 0, 0, 1 << 15, 1 << 12, 1, None, 0, None, None, 0, 0, None, None)
+    assert st == -2 and b"one launch covers" in lib.sa_last_error()
     st = lib.sa_decode(0, None, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, 0, None, 0, 0, None, 0, 0,
                        3, None, 0, 0, 1, 4, 2, 128, 64, 0.1, 1, None, 0, None)
     assert st == -5 and b"sel_rows=3" in lib.sa_last_error()
@@ -75,6 +78,13 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 3) == 3 * 2 * 4 * 130 * 4
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 1) == 0
     assert lib.sa_prefill_workspace_bytes() == 8
+    # the no-allocation decode refuses sizes past its scratch array before anything else (NULL tensors:
+    # a call let through would stop at sa_decode's own NULL check, a different status)
+    cap = int(lib.sa_decode_noalloc_scratch_bytes())
+    B = cap // (16 * 32 * 130 * 4) + 1
+    st = lib.sa_decode_noalloc(0, None, 4096, 128, None, None, 8192, 8192, 128, None, 256, 256, 1 << 20, None, 0,
+                               None, 8 * 16, 16, None, 16, 2, 8, None, 4096, 128, B, 32, 8, 128, 64, 0.088, 16, None)
+    assert st == -7 and b"scratch bytes" in lib.sa_last_error()
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

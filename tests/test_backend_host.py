@@ -79,9 +79,9 @@ def test_injected_fallback_takes_what_the_kernels_cannot(what):
     assert qs == ks == vs == (1, 4, 64, 64) and dt == q.dtype and kind == meta.kind
 
 
-def _gpu_like(dtype=torch.bfloat16):
+def _gpu_like(dtype=torch.bfloat16, head_dim=64):
     """What unsupported_reason reads of a GPU tensor (no GPU here)."""
-    return SimpleNamespace(is_cuda=True, dtype=dtype)
+    return SimpleNamespace(is_cuda=True, dtype=dtype, size=lambda d: head_dim if d == -1 else 1)
 
 
 def test_fallback_instance_and_no_fallback_still_raises():
@@ -103,4 +103,5 @@ def test_reasons_name_each_unsupported_input():
     assert "block_size" in reason(_gpu_like(), PatternMetadata(kind="mask", block_size=None))
     assert "schedule" in reason(_gpu_like(), PatternMetadata(kind="mask", block_size=64))
     assert reason(_gpu_like(), PatternMetadata(kind="dense")) is None
+    assert "head dim 96" in reason(_gpu_like(head_dim=96), PatternMetadata(kind="dense"))
     assert reason(_gpu_like(torch.float16), _csr_meta(1)) is None

@@ -101,3 +101,32 @@ def test_toy_decoder_cached_decode_matches_full_forward():
     assert torch.allclose(last, full[:, 19:], atol=1e-5)
     cache.truncate(19)
     assert cache.seq_len(0) == 19 and torch.allclose(model(ids[:, 19:], kv_cache=cache, pos_offset=19), last)
+
+
+@torch.no_grad()
+def test_toy_decoder_reference_attribute_path_and_state_dict_keys():
+    """The reference's decoder runner reads ``model.blocks[0].attn.backend.actual_backend`` after a
+    forward and copies weights with ``load_state_dict`` (decoder_sweep_runner.py:101-116); the
+    checkpoint keys are those of sparse_attentions/models/decoder_block.py."""
+    torch.manual_seed(0)
+    kw = dict(vocab_size=50, d_model=32, num_heads=4, num_layers=2, max_seq_len=24)
+    a = ToyDecoder(pattern=DenseCausalPattern(), backend=get_backend(ORACLE), **kw).eval()
+    b = ToyDecoder(pattern=DenseCausalPattern(), backend=get_backend(ORACLE), **kw).eval()
+    keys = set(a.state_dict())
+    per_block = {"norm1.weight", "norm2.weight", "mlp.fc1.weight", "mlp.fc2.weight",
+                 "attn.q_proj.weight", "attn.k_proj.weight", "attn.v_proj.weight", "attn.o_proj.weight"}
+    want = {"token_emb.weight", "pos_emb.weight", "norm_f.weight", "lm_head.weight"}
+    want |= {f"blocks.{i}.{k}" for i in range(2) for k in per_block}
+    assert keys == want, keys ^ want
+    assert a.lm_head.weight is a.token_emb.weight                        # tied head
+    ids = torch.randint(0, 50, (2, 10), generator=torch.Generator().manual_seed(3))
+    b.load_state_dict(a.state_dict())
+    assert torch.equal(a(ids), b(ids))
+    assert a.blocks[0].attn.backend.actual_backend == get_backend(ORACLE).actual_backend
+    # RMSNorm is x / sqrt(mean(x^2) + eps) * weight, MLP is fc2(gelu(fc1(x)))
+    x = torch.randn(3, 32)
+    n = a.blocks[1].norm2
+    n.weight.copy_(torch.rand(32) + 0.5)
+    assert torch.allclose(n(x), x / x.pow(2).mean(-1, keepdim=True).add(1e-6).sqrt() * n.weight, atol=1e-6)
+    m = a.blocks[0].mlp
+    assert torch.allclose(m(x), torch.nn.functional.gelu(x @ m.fc1.weight.T) @ m.fc2.weight.T, atol=1e-6)

@@ -189,6 +189,37 @@ def test_qwen3_config_helpers():
     assert not is_plain_causal_mask(causal, 3, 5)
 
 
+@torch.no_grad()
+def test_qwen3_kernel_backend_falls_back_on_cpu_fp32_with_injected_backend():
+    """The reference layer warns once and still calls its backend, which runs the masked path, when
+    no candidate passes validation (modeling_sparse_qwen3.py:259-299): a CPU fp32 model on the
+    kernel backend with an injected masked backend matches HF eager and reports the fallback."""
+    cfg, hf, _ = _tiny_models()
+    sp = copy.deepcopy(hf)
+    replace_qwen3_attention_with_sparse(sp.model, backend_name="hip_block_sparse",
+                                        fallback=oracle_backend.OracleBackend)
+    ids = torch.randint(0, 97, (2, 24), generator=torch.Generator().manual_seed(5))
+    with pytest.warns(UserWarning, match="fall back instead of using the HIP kernel") as rec:
+        got = sp(ids).logits
+        sp(ids)                                                     # warned once per layer, not per call
+    assert len(rec) == cfg.num_hidden_layers
+    assert torch.allclose(got, hf(ids).logits, atol=1e-5, rtol=0)
+    for layer in sp.model.layers:
+        attn = layer.self_attn
+        assert attn.backend_name == "hip_block_sparse"
+        assert attn.sparse_backend.actual_backend == "masked_sdpa_fallback"
+    # the same through the model class and the package registry's register_into
+    from sparseattentioninfer_amd import attention as attn_pkg
+    registry = dict(attn_pkg._REGISTRY)
+    attn_pkg.register_into(registry, fallback=oracle_backend.OracleBackend)
+    assert registry["hip_block_sparse"].default_fallback is oracle_backend.OracleBackend
+    # without a fallback the kernel backend refuses CPU tensors, as before
+    bare = copy.deepcopy(hf)
+    replace_qwen3_attention_with_sparse(bare.model, backend_name="hip_block_sparse")
+    with pytest.warns(UserWarning), pytest.raises(RuntimeError, match="no fallback backend was given"):
+        bare(ids)
+
+
 def test_hip_backend_refuses_cpu_tensors():
     from sparseattentioninfer_amd.attention import get_backend
     x = torch.zeros(1, 2, 4, 64, dtype=torch.bfloat16)
@@ -215,6 +246,18 @@ def test_group_sparsity_spec_precedence_and_parsing(tmp_path):
         GroupSparsitySpec.parse_layers('{"a": 1}')
     with pytest.raises(ValueError, match="0 <= sparsity < 1"):
         GroupSparsitySpec.build(None, [[0.5], [-0.1]])
+    # a config value is validated only where it is used (modeling_sparse_qwen3.py:123-141, :358-376):
+    # an invalid model-wide default next to a valid per-layer entry
+    bad = SimpleNamespace(sparse_attention_group_sparsities=[1.5], sparse_attention_layer_group_sparsities=[[0.3]])
+    assert GroupSparsitySpec.resolve_layer(bad, 0) == (0.3,)
+    with pytest.raises(ValueError, match="0 <= sparsity < 1"):
+        GroupSparsitySpec.resolve_layer(bad, 1)                   # layer 1 falls back to the invalid default
+    assert GroupSparsitySpec.with_config_defaults(bad, [0.4]).for_layer(1) == (0.4,)   # argument replaces it
+    with pytest.raises(ValueError, match="0 <= sparsity < 1"):
+        GroupSparsitySpec.with_config_defaults(bad)
+    bad_layers = SimpleNamespace(sparse_attention_group_sparsities=[0.2],
+                                 sparse_attention_layer_group_sparsities=[[2.0]])
+    assert GroupSparsitySpec.with_config_defaults(bad_layers, None, [[0.1]]).for_layer(0) == (0.1,)
     out = SimpleNamespace()
     merged.write_to(out)
     assert out.sparse_attention_group_sparsities == [0.1, 0.2]

@@ -6,9 +6,9 @@ layers 0-17 and dense causal in 18-35, batch 8, an 8192-token prompt, paged KV c
   and the reference's dense-masked arithmetic (fp32, row-chunked) on the same q/k/v and passes the
   oracle's result on, so each layer's kernel sees exactly the oracle path's inputs.  Every layer's
   attention core, in the prompt forward and in paged decode steps, must meet the kernel tolerance
-  against the fp32 oracle: mean-abs 2e-3, and every element within max(2e-2, one bf16 ulp of the
-  oracle value, at most 2^-7 of it) -- the deeper layers of the random-init model produce attention outputs above 4,
-  where one bf16 ulp (3.1e-2) is already wider than the absolute 2e-2.
+  against the fp32 oracle: max-abs 2e-2 and mean-abs 2e-3.  The error relative to one bf16 ulp of
+  the oracle value is printed beside it (the deeper layers of the random-init model produce
+  attention outputs above 4, where one bf16 ulp is 3.1e-2).
 * The logit max-abs difference of the all-kernel model against that oracle path (the reference's
   sparse path, which cannot run on this machine) is reported at the stated size
   (``sparse_llm/common/benchmark/generation.py:232-271`` defines the metrics).
@@ -20,7 +20,7 @@ import torch
 
 from sparseattentioninfer_amd.qwen3 import PagedKVCache
 from sparseattentioninfer_amd.qwen3.runtime import build_model, qwen3_config
-from tests.helpers import MEAN_ABS
+from tests.helpers import MAX_ABS, MEAN_ABS
 from tests.twin_backend import TwinBackend
 
 pytestmark = pytest.mark.gpu
@@ -67,13 +67,13 @@ def test_configs_4_stated_size_teacher_forced_layers_and_logits():
         recs = [t.records[-1] for t in twins]
         worst_max = max(r["max_abs"] for r in recs)
         worst_mean = max(r["mean_abs"] for r in recs)
-        worst_bound = max(r["bound"] for r in recs)
+        worst_ulp = max(r["ulp_ratio"] for r in recs)
         scale = max(r["out_scale"] for r in recs)
         _say(f"[e2e] {'prompt' if s == 0 else f'decode step {s}'}: worst layer attention max-abs {worst_max:.3e}, "
-             f"mean-abs {worst_mean:.3e}, error / max(2e-2, 2^-7 |oracle|) {worst_bound:.3f} over {len(recs)} layers "
+             f"mean-abs {worst_mean:.3e}, error / max(2e-2, 2^-7 |oracle|) {worst_ulp:.3f} over {len(recs)} layers "
              f"(largest attention output {scale:.2f})")
         for i, r in enumerate(recs):
-            assert r["bound"] <= 1.0 and r["mean_abs"] <= MEAN_ABS, (s, i, r)
+            assert r["max_abs"] <= MAX_ABS and r["mean_abs"] <= MEAN_ABS, (s, i, r)
     assert all(t.last_kernel == "decode" for t in twins)
     del cache
     torch.cuda.empty_cache()
@@ -90,5 +90,6 @@ def test_configs_4_stated_size_teacher_forced_layers_and_logits():
         _say(f"[e2e] {'prompt' if s == 0 else f'decode step {s}'}: logit max-abs diff {diff:.4e} "
              f"(logit scale {scale:.3e}), top-1 agreement {agree:.3f}")
         assert torch.isfinite(lg).all()
-        # bf16 activations over 36 layers compound; each layer is held to the kernel tolerance above
-        assert diff <= 0.15 * max(1.0, scale), (s, diff, scale)
+        # bf16 activations over 36 layers compound (measured 4.3-4.8 % of the logit scale); each
+        # layer is held to the kernel tolerance above
+        assert diff <= 0.1 * max(1.0, scale), (s, diff, scale)

@@ -72,9 +72,11 @@ def test_noalloc_refuses_sizes_past_its_scratch():
     cap = int(lib.sa_decode_noalloc_scratch_bytes())
     B = cap // (16 * 32 * 130 * 4) + 1          # 16 splits of [B, 32, 130] fp32 partials exceed it
     assert lib.sa_decode_workspace_bytes(B, 32, 128, 16) > cap
-    fake = 256   # never dereferenced: the call returns before any device work
-    args = [0, fake, 4096, 128, fake, fake, 8192, 8192, 128, fake, 256, 256, 1 << 20, fake, 0,
-            fake, 8 * 16, 16, fake, 16, 2, 8, fake, 4096, 128, B, 32, 8, 128, 64, 0.088, 16,
+    # NULL tensors: the size check returns first; were it ever to let the call through, sa_decode's
+    # own NULL check would refuse it (a different status) before any launch
+    null = None
+    args = [0, null, 4096, 128, null, null, 8192, 8192, 128, null, 256, 256, 1 << 20, null, 0,
+            null, 8 * 16, 16, null, 16, 2, 8, null, 4096, 128, B, 32, 8, 128, 64, 0.088, 16,
             torch.cuda.current_stream().cuda_stream]
     st = lib.sa_decode_noalloc(*args)
     assert st == -7 and b"scratch bytes" in lib.sa_last_error()

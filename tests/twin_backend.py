@@ -59,14 +59,14 @@ class TwinBackend(AttentionBackend):
         return self.hip.last_kernel
 
     def _pick(self, got, want, T_q, T_k, kind):
-        """Records the kernel's error against the fp32 oracle: max-abs, mean-abs and ``bound`` = the
-        worst ratio of an element's error to max(2e-2, 2^-7 |oracle|), i.e. the BASELINE absolute
-        tolerance, widened to one bf16 ulp (of the binade's top) where the output exceeds 2.56 (one bf16
-        ulp of a value in [4, 8) is already 3.1e-2)."""
+        """Records the kernel's error against the fp32 oracle: max-abs and mean-abs (the quantities the
+        tests hold to the absolute tolerances 2e-2 and 2e-3) and, as a printed diagnostic only,
+        ``ulp_ratio`` = the worst ratio of an element's error to max(2e-2, 2^-7 |oracle|), the error
+        relative to one bf16 ulp where the output exceeds 2.56."""
         d = (got.float() - want).abs()
         allow = torch.clamp(want.abs() * 2.0 ** -7, min=2e-2)
         self.records.append({"T_q": T_q, "T_k": T_k, "kind": kind, "max_abs": d.max().item(),
-                             "mean_abs": d.mean().item(), "bound": (d / allow).max().item(),
+                             "mean_abs": d.mean().item(), "ulp_ratio": (d / allow).max().item(),
                              "out_scale": want.abs().max().item()})
         return want.to(got.dtype) if self.returns == "oracle" else got
 
