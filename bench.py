@@ -714,11 +714,11 @@ def main():
             cb1 = cpu_baseline(c1, args.cpu_seconds / 3, "configs[1]")
             cb1["value"] = round(cb1["value"], 5)
             line["configs1"]["cpu_baseline"] = cb1
-        del c1
         if pre is None and args.only == "bernoulli":
             line.update(value=round(c1["tflops"], 3), ms_per_step=round(c1["ms_per_step"], 4),
                         config={"workload": c1["workload"], "kernel_us": round(c1["kernel_us"], 2)},
                         roofline=line["configs1"]["roofline"])
+        del c1
     if args.only in ("all", "decode"):
         dec = run_decode(args, dev)
         dec["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in dec["roofline"].items()}

@@ -222,6 +222,9 @@ struct Prefill {
   static constexpr int LDS_KV = (NBK + NBV) * TILE_BYTES;
   static constexpr int LDS_Q = PIPE ? NW * WAVE_BYTES : 16;
   static constexpr float RESCALE_LOG2 = 8.f;
+  // Pipelined loop: the row reference is refit when one lane's probabilities of a tile (32 of a
+  // row's keys) sum past this; below it no probability exceeds 2^16, far from fp32 / bf16 overflow.
+  static constexpr float REFIT_SUM = 65536.f;
   static_assert(NI % NW == 0, "direct loads must split evenly over the waves");
   static_assert(NW * WAVE_BYTES <= LDS_KV, "the epilogue stages O in the K/V buffers");
 
@@ -776,23 +779,6 @@ struct Prefill {
     return mx * c;  // -inf stays -inf (c > 0)
   }
 
-  // Raises the row reference when the tile's max exceeds it by more than 2^RESCALE_LOG2
-  // (rare; rescales O and l) and returns -m_ref for the exponent.
-  static __device__ __forceinline__ float update_ref(float m_tile, float& m_ref, float& l_run,
-                                                     f32x16 (&O)[D / 32]) {
-    float m = m_ref == -__builtin_inff() ? m_tile : m_ref;
-    if (__any(m_tile > m + RESCALE_LOG2)) {
-      const float m_new = fmaxf(m, m_tile);
-      const float alpha = m_new == -__builtin_inff() ? 1.f : fast_exp2(m - m_new);
-      m = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) O[dt] *= alpha;
-    }
-    m_ref = m;
-    return m == -__builtin_inff() ? 0.f : -m;
-  }
-
   // ---- lookahead metadata (persistent four-head loop) -----------------------------------
   // While an item's first tiles load, the persistent loop fetches the CSR row of the next
   // item, the CSR offsets and decoded (qt, r, hs, b) of the item after it and a new claim
@@ -945,7 +931,6 @@ struct Prefill {
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) Qr[cc] = qfrag(sQw, f, cc);
     f32x16 S[2] = {f32x16{}, f32x16{}};  // scores of the current tile
-    float mt_cur = -__builtin_inff();
     if (has_cur) {
 #pragma unroll
       for (int cc = 0; cc < D / 16; ++cc) {
@@ -953,8 +938,12 @@ struct Prefill {
 #pragma unroll
         for (int j = 0; j < 2; ++j) S[j] = E::mfma32(kfrag(sK, f, j, cc), qv, S[j]);
       }
-      mt_cur = mask_rowmax(a, S, row_bits(a, m_cur, it.hf, it.l32), lim0 - kt_cur * KT, c);
+      // The row reference is the first tile's (masked) row max; later tiles keep it unless their
+      // probabilities grow past REFIT_SUM (refit below).
+      m_ref = mask_rowmax(a, S, row_bits(a, m_cur, it.hf, it.l32), lim0 - kt_cur * KT, c);
     }
+    float neg_m = m_ref == -__builtin_inff() ? 0.f : -m_ref;
+    bool ref_ok = !__any(m_ref == -__builtin_inff());  // every row of the wave has a reference
     // The first step loads K of tile t2 into the buffer of t0, which the prime just read.
     __syncthreads();
 
@@ -973,30 +962,61 @@ struct Prefill {
     constexpr int PE = 32 / NQ;  // probabilities per QK MFMA
     constexpr int NP = D / 8;    // PV MFMAs: i -> (dt = i % (D/32), h, j)
     constexpr int ND = D / 32;
-    constexpr int ME = 32 / NP;  // scores reduced per PV MFMA
 
     // Block B: PV of the tile in V buffer cV with probabilities P (D/8 MFMAs; V fragments
-    // read two MFMAs ahead), with the scaled row max of R (masked scores) spread over it.
-    auto block_b = [&](const char* cV, const f32x16 (&R)[2]) -> float {
+    // read two MFMAs ahead).  No VALU work: the row reference stays fixed between refits.
+    auto block_b = [&](const char* cV) {
       auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
       u32x4 vf[2] = {vfr(0), vfr(1)};
-      float mx = -__builtin_inff();
       __builtin_amdgcn_s_setprio(0);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NP; ++i) {
         O[i % ND] = E::mfma32(vf[i & 1], P[i / (2 * ND)][(i / ND) & 1], O[i % ND]);
         if (i + 2 < NP) vf[i & 1] = vfr(i + 2);
-#pragma unroll
-        for (int u = 0; u < ME; ++u) {
-          const int x = ME * i + u;
-          mx = fmaxf(mx, R[x >> 4][x & 15]);
-        }
-        asm volatile("" : "+v"(mx));  // keeps the reduction spread over the MFMAs
         __builtin_amdgcn_sched_barrier(0);
       }
-      mx = halves_max(mx);
-      return mx * c;
+    };
+
+    // Probabilities of the tile whose masked scores are Sc, against the current reference:
+    // P and this lane's share of the row sum.
+    auto probs = [&](const f32x16 (&Sc)[2], float& ls) {
+      uint32_t pw[2][2][4];
+      ls = 0.f;
+#pragma unroll
+      for (int x = 0; x < 32; x += 2) {
+        const int j = x >> 4, rr = x & 15;
+        const float p0 = fast_exp2(fmaf(Sc[j][rr], c, neg_m));
+        const float p1 = fast_exp2(fmaf(Sc[j][rr + 1], c, neg_m));
+        ls += p0 + p1;
+        pw[j][rr >> 3][(rr & 7) >> 1] = E::pack2f(p0, p1);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) P[j][h] = u32x4{pw[j][h][0], pw[j][h][1], pw[j][h][2], pw[j][h][3]};
+    };
+
+    // Refit (rare): a row had no reference yet, or a lane's probabilities of this tile sum past
+    // REFIT_SUM (or to inf / NaN).  Raises each row's reference to its max over this tile, rescales
+    // O and l to it and recomputes the tile's probabilities.  Any reference gives the same result
+    // up to rounding; the refit only keeps 2^(s c - m_ref) finite.
+    auto refit = [&](const f32x16 (&Sc)[2], float& ls) {
+      float mx = Sc[0][0];
+#pragma unroll
+      for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, Sc[0][rr]);
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) mx = fmaxf(mx, Sc[1][rr]);
+      const float m_tile = halves_max(mx) * c;  // -inf stays -inf (c > 0)
+      const float m_new = m_ref == -__builtin_inff() ? m_tile : fmaxf(m_ref, m_tile);
+      const float alpha = (m_ref == -__builtin_inff() || m_new == -__builtin_inff()) ? 1.f : fast_exp2(m_ref - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt) O[dt] *= alpha;
+      m_ref = m_new;
+      neg_m = m_ref == -__builtin_inff() ? 0.f : -m_ref;
+      ref_ok = !__any(m_ref == -__builtin_inff());
+      probs(Sc, ls);
     };
 
     // One step on the tile whose scores are in Sc and whose K is in buffer KB, filling Sx
@@ -1013,10 +1033,9 @@ struct Prefill {
       if (has_nn) load_k(kt_nn, kb_cur);
       if (has_nxt) load_v(kt_nxt, vb_nxt);
 
-      // Upper half: B of the previous tile; the row max it reduces is this tile's.
-      if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, Sc);
+      // Upper half: B of the previous tile.
+      if (lag && pending) block_b(sV + vb_prev * TILE_BYTES);
 
-      const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
       const char* cK = sK + kb_nxt * TILE_BYTES;
       // Branch-free on purpose: after the last tile the QK half runs on a stale K buffer
       // (no direct load is in flight then) and its result is dropped.  A separate last-tile
@@ -1056,11 +1075,12 @@ struct Prefill {
         }
         __builtin_amdgcn_sched_barrier(0);
       }
-      l_run += ls;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int h = 0; h < 2; ++h) P[j][h] = u32x4{pw[j][h][0], pw[j][h][1], pw[j][h][2], pw[j][h][3]};
+      if (!ref_ok || __any(!(ls <= REFIT_SUM))) refit(Sc, ls);
+      l_run += ls;
 
       // Causal / T_k mask of the next tile, only where it cuts into the tile (uniform per
       // wave; about one tile in a row's window).
@@ -1069,8 +1089,8 @@ struct Prefill {
         mask_tile(a, Sx, row_bits(a, m_nxt, it.hf, it.l32), lim0 - kbase_n);
       }
 
-      // Lower half: B of this tile; the row max it reduces is the next tile's.
-      if (!lag) mt_cur = block_b(sV + vb_cur * TILE_BYTES, Sx);
+      // Lower half: B of this tile.
+      if (!lag) block_b(sV + vb_cur * TILE_BYTES);
       pending = true;
 
       wait_dma();
@@ -1099,23 +1119,11 @@ struct Prefill {
     // tile runs after it.
     auto last_step = [&](f32x16 (&Sc)[2]) {
       const int vb_prev = vb_cur == 0 ? 2 : vb_cur - 1;
-      if (lag && pending) mt_cur = block_b(sV + vb_prev * TILE_BYTES, Sc);
-      const float neg_m = update_ref(mt_cur, m_ref, l_run, O);
-      float ls = 0.f;
-      uint32_t pw[2][2][4];
-#pragma unroll
-      for (int x = 0; x < 32; x += 2) {
-        const int j = x >> 4, rr = x & 15;
-        const float p0 = fast_exp2(fmaf(Sc[j][rr], c, neg_m));
-        const float p1 = fast_exp2(fmaf(Sc[j][rr + 1], c, neg_m));
-        ls += p0 + p1;
-        pw[j][rr >> 3][(rr & 7) >> 1] = E::pack2f(p0, p1);
-      }
+      if (lag && pending) block_b(sV + vb_prev * TILE_BYTES);
+      float ls;
+      probs(Sc, ls);
+      if (!ref_ok || __any(!(ls <= REFIT_SUM))) refit(Sc, ls);
       l_run += ls;
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int h = 0; h < 2; ++h) P[j][h] = u32x4{pw[j][h][0], pw[j][h][1], pw[j][h][2], pw[j][h][3]};
       if (!lag) block_pv(sV + vb_cur * TILE_BYTES);
     };
 

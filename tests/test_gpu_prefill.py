@@ -72,6 +72,27 @@ def test_prefill_matches_oracle(case):
     assert_close_bf16(out, want, name)
 
 
+@pytest.mark.parametrize("boost", [8.0, 100.0])
+def test_row_reference_refit_when_later_keys_dominate(boost):
+    """The four-head loop keeps each row's softmax reference from its first tile and refits it only
+    when a later tile's probabilities sum past 2^16 (x8: scores up to ~2^20 above the reference) or
+    overflow to inf (x100).  Keys of blocks 3 and later are scaled by ``boost``, so nearly every row
+    refits, some more than once; the result must still match the fp32 oracle."""
+    B, Hq, Hkv, T, D, bs = 1, 8, 2, 1000, 128, 64
+    _say(f"[prefill] refit boost {boost}")
+    bm = _mask("bernoulli0.4", Hkv, T, T, bs, seed=13)
+    pairs, offsets = block_mask_to_csr(bm)
+    q, k, v = _case_inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=21)
+    k = k.float()
+    k[:, :, 3 * bs:] *= boost * torch.linspace(0.5, 1.0, T - 3 * bs)[None, None, :, None]
+    k = k.to(torch.bfloat16)
+    out = ops.universal_sparse_attn(q.to(DEV), k.to(DEV), v.to(DEV), pairs.to(DEV), offsets.to(DEV), bs)
+    torch.cuda.synchronize()
+    want = oa.block_sparse_attention(q.to(DEV), k.to(DEV), v.to(DEV), pairs, offsets, bs)
+    assert torch.isfinite(out.float()).all()
+    assert_close_bf16(out, want, f"refit x{boost}")
+
+
 @pytest.mark.parametrize("name", ["cfg1_trailing", "gqa_group_ragged"])
 def test_prefill_matches_dense_masked_sdpa(name):
     """Direct parity with the reference's dense masked semantics (masked_sdpa.py:23-68)."""
