@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 4
+#define SA_ABI_VERSION 5
 
 /* element types */
 #define SA_DTYPE_BF16 0
@@ -81,10 +81,15 @@ const char* sa_last_error(void);
  *
  * workspace (optional, sa_prefill_workspace_bytes() bytes, 4-byte aligned):
  * with it the kernel runs one persistent workgroup per resident slot that
- * claims work items from a counter pair in the workspace.  It must be zeroed
- * before its first use; every completed launch leaves it zeroed again.
- * Launches that may run concurrently must not share one workspace.  NULL
- * launches one workgroup per work item instead.
+ * claims work items from counters in the workspace.  It must be zeroed before
+ * its first use; every completed launch leaves its counters zeroed again.
+ * Launches that may run concurrently (other streams, graph replays on other
+ * streams) must not share one workspace: keep one per stream.  Word 3 of the
+ * workspace is a status word that launches only set and the caller clears:
+ * bit 0 means a launch processed fewer work items than it has (its counters
+ * were not zero at launch, or an overlapping launch shared them) and left the
+ * skipped items' outputs unwritten.  NULL launches one workgroup per work
+ * item instead.
  */
 int sa_prefill(int dtype,
                const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
@@ -100,7 +105,7 @@ int sa_prefill(int dtype,
                void* workspace, int64_t workspace_bytes,
                void* stream);
 
-/* Bytes of the optional sa_prefill workspace (a counter pair). */
+/* Bytes of the optional sa_prefill workspace (counters and the status word). */
 int64_t sa_prefill_workspace_bytes(void);
 
 /*

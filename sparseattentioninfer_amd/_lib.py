@@ -11,7 +11,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 

@@ -79,7 +79,9 @@ struct PrefillArgs {
   int tpb_log2;      // log2(block_size / 64): key tiles per CSR block
   int q_offset;
   float scale_log2;  // sm_scale * log2(e)
-  unsigned int* counter;  // persistent mode: 2 zeroed counters (next item, finished workgroups)
+  // Persistent mode: the workspace words (WS_* below), zero at launch; every completed launch
+  // leaves the counters zero and the status word as it found it, or with WS_SKIPPED set.
+  unsigned int* counter;
   // Work-item decoding without integer division: per_tile = R * B * head_splits, and
   // floor((2^32 - 1) / d) for d = per_tile, R, head_splits (see fast_div).
   int per_tile;
@@ -95,6 +97,14 @@ struct PrefillArgs {
   int q_split, head_items, per_group, bhs;
   uint32_t mul_group, mul_bhs;
 };
+
+// Words of the persistent-launch workspace: the next unclaimed item, the workgroups done, the
+// items processed, and a status word that only the host clears.  A launch whose workgroups
+// processed fewer items than it has (the counters were not zero at launch, or two launches
+// that overlapped in time shared them) sets WS_SKIPPED: the skipped items' outputs are not
+// written, so the caller must not use the output.
+enum : int { WS_NEXT = 0, WS_DONE_WG = 1, WS_DONE_ITEMS = 2, WS_STATUS = 3, WS_WORDS = 8 };
+constexpr unsigned WS_SKIPPED = 1u;
 
 // CSR rows of a persistent launch in descending order of retained blocks (row_order).
 constexpr int MAX_ORDERED_ROWS = 256;
@@ -830,7 +840,7 @@ struct Prefill {
         ld.o0 = o[0];
         ld.o1 = o[1];
       }
-      ld.nv = atomicAdd(a.counter, 1u);
+      ld.nv = atomicAdd(&a.counter[WS_NEXT], 1u);
     }
   }
 
@@ -1222,16 +1232,17 @@ struct Prefill {
   // row of item i + 1, the offsets and (qt, r, hs, b) of item i + 2 and claims item i + 3
   // (Look).  Claims only grow, so the first id past the end ends the loop in every wave at
   // once.
-  static __device__ __forceinline__ void run_lookahead(const PrefillArgs& a, int n_items, char* sKV, char* sQ,
-                                                       int32_t* s_row, int32_t* s_mask) {
+  static __device__ __forceinline__ int run_lookahead(const PrefillArgs& a, int n_items, char* sKV, char* sQ,
+                                                      int32_t* s_row, int32_t* s_mask) {
+    int done = 0;  // items this workgroup processed
     // Per slot k = item index mod 4: id, CSR offsets (first, end) and (qt, r, hs, b); the loop
     // top reads an item's whole slot (and the ids and offsets of the next two) in one batch.
     __shared__ __attribute__((aligned(16))) int s_meta[4][8];
     const int tid = threadIdx.x;
     if (tid == 0) {
-      const unsigned v0 = atomicAdd(&a.counter[0], 1u);
-      const unsigned v1 = atomicAdd(&a.counter[0], 1u);
-      const unsigned v2 = atomicAdd(&a.counter[0], 1u);
+      const unsigned v0 = atomicAdd(&a.counter[WS_NEXT], 1u);
+      const unsigned v1 = atomicAdd(&a.counter[WS_NEXT], 1u);
+      const unsigned v2 = atomicAdd(&a.counter[WS_NEXT], 1u);
       s_meta[0][0] = (int)v0;
       s_meta[1][0] = (int)v1;
       s_meta[2][0] = (int)v2;
@@ -1296,7 +1307,9 @@ struct Prefill {
       const int b = __builtin_amdgcn_readfirstlane(m0b.z);
       item_pipelined<true>(a, qt, r, hs, b, sKV, sQ, s_row + (i & 1) * RC, SUB ? s_mask + (i & 1) * RC : s_mask,
                            &lk);
+      ++done;
     }
+    return done;
   }
 
   static __device__ void run(const PrefillArgs& a) {
@@ -1326,21 +1339,32 @@ struct Prefill {
     // Persistent: claim items from a counter until none is left.  The last workgroup to
     // finish resets the counter pair to zero for the next launch on the stream.
     if (a.row_order) rank_rows(a, reinterpret_cast<int*>(sKV));  // K/V buffers are free here
+    int done = 0;
     if constexpr (PIPE) {
-      run_lookahead(a, n_items, sKV, sQ, s_row, s_mask);
+      done = run_lookahead(a, n_items, sKV, sQ, s_row, s_mask);
     } else {
       for (;;) {
-        if (threadIdx.x == 0) s_item = (int)atomicAdd(&a.counter[0], 1u);
+        if (threadIdx.x == 0) s_item = (int)atomicAdd(&a.counter[WS_NEXT], 1u);
         __syncthreads();
         const int v = s_item;
         __syncthreads();
         if (v >= n_items) break;
         process(a, v, sKV, sQ, s_row, s_mask);
+        ++done;
       }
     }
-    if (threadIdx.x == 0 && atomicAdd(&a.counter[1], 1u) == gridDim.x - 1) {
-      atomicExch(&a.counter[0], 0u);
-      atomicExch(&a.counter[1], 0u);
+    // Items processed, then this workgroup done; the last one checks the total and zeroes the
+    // counters for the next launch on the stream.
+    if (threadIdx.x == 0) {
+      atomicAdd(&a.counter[WS_DONE_ITEMS], (unsigned)done);
+      __threadfence();
+      if (atomicAdd(&a.counter[WS_DONE_WG], 1u) == gridDim.x - 1) {
+        __threadfence();
+        if (atomicAdd(&a.counter[WS_DONE_ITEMS], 0u) != (unsigned)n_items) atomicOr(&a.counter[WS_STATUS], WS_SKIPPED);
+        atomicExch(&a.counter[WS_NEXT], 0u);
+        atomicExch(&a.counter[WS_DONE_ITEMS], 0u);
+        atomicExch(&a.counter[WS_DONE_WG], 0u);
+      }
     }
   }
 };
@@ -1516,4 +1540,4 @@ extern "C" int sa_prefill(int dtype,
   return 0;
 }
 
-extern "C" int64_t sa_prefill_workspace_bytes(void) { return 2 * (int64_t)sizeof(unsigned int); }
+extern "C" int64_t sa_prefill_workspace_bytes(void) { return sa::WS_WORDS * (int64_t)sizeof(unsigned int); }

@@ -31,10 +31,11 @@ _PREFILL_WS: dict = {}
 
 
 def _prefill_workspace(t: torch.Tensor) -> torch.Tensor:
-    """Zeroed counter pair for the persistent prefill kernel, one per (device, stream).
+    """Zeroed workspace (counters and a status word) for the persistent prefill kernel, one per
+    (device, stream).
 
-    Each launch leaves it zeroed again; launches on one stream run in order, so
-    they can share it.
+    Each launch leaves its counters zeroed again; launches on one stream run in order, so they
+    can share it.  Launches on other streams get their own.
     """
     stream = _stream(t)
     key = (t.device.index, stream)
@@ -44,6 +45,24 @@ def _prefill_workspace(t: torch.Tensor) -> torch.Tensor:
         ws = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=t.device)
         _PREFILL_WS[key] = ws
     return ws
+
+
+PREFILL_WS_STATUS_WORD = 3    # status word of the prefill workspace (include/sparse_attn.h)
+PREFILL_WS_SKIPPED = 1        # a launch processed fewer work items than it has
+
+
+def prefill_workspace_status(device=None, clear: bool = True) -> int:
+    """Status word of the prefill workspace of the current stream on ``device`` (0: every launch
+    so far processed all its work items; bit 0: one did not, its output is incomplete).
+    Reads device memory (a synchronisation of the stream); ``clear`` resets the word."""
+    dev = torch.device("cuda", torch.cuda.current_device() if device is None else torch.device(device).index)
+    ws = _PREFILL_WS.get((dev.index, torch.cuda.current_stream(dev).cuda_stream))
+    if ws is None:
+        return 0
+    st = int(ws[PREFILL_WS_STATUS_WORD].item())
+    if clear and st:
+        ws[PREFILL_WS_STATUS_WORD].zero_()
+    return st
 
 
 class TileSchedule:

@@ -77,7 +77,7 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     assert st != 0 and b"block table of 8 columns" in lib.sa_last_error()
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 3) == 3 * 2 * 4 * 130 * 4
     assert lib.sa_decode_workspace_bytes(2, 4, 128, 1) == 0
-    assert lib.sa_prefill_workspace_bytes() == 8
+    assert lib.sa_prefill_workspace_bytes() == 32            # counters and the status word (word 3)
     # the no-allocation decode refuses sizes past its scratch array before anything else (NULL tensors:
     # a call let through would stop at sa_decode's own NULL check, a different status)
     cap = int(lib.sa_decode_noalloc_scratch_bytes())

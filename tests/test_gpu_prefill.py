@@ -72,6 +72,31 @@ def test_prefill_matches_oracle(case):
     assert_close_bf16(out, want, name)
 
 
+def test_workspace_left_nonzero_is_reported():
+    """A persistent launch whose counters are not zero at launch (a shared or stale workspace)
+    skips work items; the last workgroup notices that fewer items were processed than the launch
+    has and sets the workspace's status bit, and the counters are zero again afterwards."""
+    B, Hq, Hkv, T, D, bs = 1, 8, 2, 1000, 128, 64
+    _say("[prefill] workspace status")
+    bm = _mask("bernoulli0.3", Hkv, T, T, bs, seed=3)
+    pairs, offsets = block_mask_to_csr(bm)
+    q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=4))
+    pairs, offsets = pairs.to(DEV), offsets.to(DEV)
+    want = oa.block_sparse_attention(q, k, v, pairs.cpu(), offsets.cpu(), bs)
+    ops.universal_sparse_attn(q, k, v, pairs, offsets, bs)
+    assert ops.prefill_workspace_status() == 0
+    ws = ops._prefill_workspace(q)
+    ws[0] = 3                                   # as if another launch had claimed three items
+    ops.universal_sparse_attn(q, k, v, pairs, offsets, bs)
+    torch.cuda.synchronize()
+    assert ops.prefill_workspace_status() == ops.PREFILL_WS_SKIPPED
+    assert ws[:3].tolist() == [0, 0, 0]         # counters zero again, status cleared by the read
+    assert int(ws[ops.PREFILL_WS_STATUS_WORD].item()) == 0
+    out = ops.universal_sparse_attn(q, k, v, pairs, offsets, bs)
+    assert ops.prefill_workspace_status() == 0
+    assert_close_bf16(out, want, "after a reported launch")
+
+
 @pytest.mark.parametrize("boost", [8.0, 100.0])
 def test_row_reference_refit_when_later_keys_dominate(boost):
     """The four-head loop keeps each row's softmax reference from its first tile and refits it only
