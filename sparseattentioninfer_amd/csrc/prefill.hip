@@ -874,10 +874,14 @@ struct Prefill {
   // this wave's rows cost matrix work but add p == 0.  LOOK: the item's CSR row is already
   // in s_row (lk->e0, lk->n_ent) and the lookahead reads of *lk run under the first tiles'
   // loads.
+  // vb_first: V buffer for the item's first tile, the one that the previous item's last step
+  // does not read (K buffers are never read in an item's last step); set to the next item's on
+  // return.  So an item starts loading without waiting for the other waves to finish the
+  // previous one.
   template <bool LOOK>
   static __device__ __forceinline__ void item_pipelined(const PrefillArgs& a, int qt, int r, int hs, int b,
                                                         char* sKV, char* sQ, int32_t* s_row, int32_t* s_mask,
-                                                        const Look* lk) {
+                                                        const Look* lk, int& vb_first) {
     char* sK = sKV;
     char* sV = sKV + NBK * TILE_BYTES;
     const int lane = threadIdx.x & 63;
@@ -919,17 +923,17 @@ struct Prefill {
     };
 
     // Prime: K of the first two usable tiles in K buffers 0, 1 and V of the first in V
-    // buffer 0; S^T and row max of the first.
+    // buffer vb_first; S^T and row max of the first.  No wave reads those buffers until every
+    // wave has passed the barrier below: the K buffers were last read before the previous
+    // item's last barrier, and its last step reads only the other two V buffers.
     TileQueue q = queue_begin(a, it);
     int kt_cur = 0, kt_nxt = 0;
     uint32_t m_cur = 0u, m_nxt = 0u;
     bool has_cur = queue_pop(a, it, s_row, s_mask, q, kt_cur, m_cur);
     bool has_nxt = has_cur && queue_pop(a, it, s_row, s_mask, q, kt_nxt, m_nxt);
-    // Every wave is past the previous item's last reads of the K/V buffers.
-    if constexpr (LOOK) __syncthreads();
     if (has_cur) {
       load_k(kt_cur, 0);
-      load_v(kt_cur, 0);
+      load_v(kt_cur, vb_first);
     }
     if (has_nxt) load_k(kt_nxt, 1);
     LookLoads ld;
@@ -965,7 +969,7 @@ struct Prefill {
     // in step i by both halves, K of tile i+2 loads); V is triple-buffered (V of tiles i-1
     // and i are read, V of tile i+1 loads), so one barrier per step still suffices.
     const bool lag = it.hf == 1;  // upper half: one half-step behind
-    int vb_cur = 0;  // V buffer of the current tile (tile i in buffer i mod 3)
+    int vb_cur = vb_first;  // V buffer of the current tile (buffers in turn)
     bool pending = false;  // upper half: B of the previous tile still to run
     u32x4 P[2][2];         // probabilities of the tile whose B is next
     constexpr int NQ = D / 8;    // QK MFMAs per tile: i -> (key half j = i % 2, cc = i / 2)
@@ -1155,6 +1159,7 @@ struct Prefill {
       last_step(S);
       // Upper half: PV of the last tile.
       if (lag) block_pv(sV + vb_cur * TILE_BYTES);
+      vb_first = vb_cur == 2 ? 0 : vb_cur + 1;  // read by neither half in the last step
     }
     // O is staged in the wave's own Q slot (Q is in registers): no other wave touches it.
     epilogue(a, it, b, O, l_run, sQw, lane);
@@ -1221,7 +1226,10 @@ struct Prefill {
     int qt, r, hs, b;
     decode_item_uniform(a, v, qt, r, hs, b);
     if constexpr (PIPE)
-      item_pipelined<false>(a, qt, r, hs, b, sKV, sQ, s_row, s_mask, nullptr);
+    {
+      int vb_first = 0;
+      item_pipelined<false>(a, qt, r, hs, b, sKV, sQ, s_row, s_mask, nullptr, vb_first);
+    }
     else
       item(a, qt, r, hs, b, sKV, s_row, s_mask);
   }
@@ -1234,7 +1242,8 @@ struct Prefill {
   // once.
   static __device__ __forceinline__ int run_lookahead(const PrefillArgs& a, int n_items, char* sKV, char* sQ,
                                                       int32_t* s_row, int32_t* s_mask) {
-    int done = 0;  // items this workgroup processed
+    int done = 0;      // items this workgroup processed
+    int vb_first = 0;  // V buffer free for the next item's first tile
     // Per slot k = item index mod 4: id, CSR offsets (first, end) and (qt, r, hs, b); the loop
     // top reads an item's whole slot (and the ids and offsets of the next two) in one batch.
     __shared__ __attribute__((aligned(16))) int s_meta[4][8];
@@ -1306,7 +1315,7 @@ struct Prefill {
       const int hs = __builtin_amdgcn_readfirstlane(m0b.y);
       const int b = __builtin_amdgcn_readfirstlane(m0b.z);
       item_pipelined<true>(a, qt, r, hs, b, sKV, sQ, s_row + (i & 1) * RC, SUB ? s_mask + (i & 1) * RC : s_mask,
-                           &lk);
+                           &lk, vb_first);
       ++done;
     }
     return done;
