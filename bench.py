@@ -602,7 +602,10 @@ def run_e2e(args, dev):
             "decode": "HIP graph replay per token (two eager warm-up steps and the capture included in the total)",
             "decode_tok_per_s_eager": eager_tps,
             "decode_ms_per_step_median_eager": 1e3 * eager_times[len(eager_times) // 2],
-            "kv_cache_gb": kv_bytes / 1e9, "model_build_s": build_s}
+            "kv_cache_gb": kv_bytes / 1e9, "model_build_s": build_s,
+            # GraphDecoder set-up before the first step (each sparse layer's decode selection for
+            # every position of the generation, the captures are part of the steps)
+            "graph_setup_s": gg["graph_setup_s"]}
 
 
 def copy_calibration(dev):

@@ -22,8 +22,11 @@
 //    under the current tile's O^T += V^T P^T; Q is staged in LDS there to leave the
 //    registers to the accumulators.  Smaller workgroups run one tile at a time;
 //  * the softmax works in base 2 with scale*log2(e) folded into one FMA before the
-//    hardware v_exp_f32 (2^x); the row reference max is only raised (and O rescaled) when
-//    a row max exceeds it by more than 2^8, so the common case never touches O with VALU;
+//    hardware v_exp_f32 (2^x).  Four-head workgroups take each row's reference from its
+//    first tile's (masked) max and refit it (raise it to the tile max, rescale O and l)
+//    only when a lane's probabilities of one tile sum past 2^16 or overflow; smaller
+//    workgroups raise it when a row max exceeds it by more than 2^8.  Either way the
+//    common case never touches O with VALU;
 //  * O is written back through LDS so that every global store is a 16-byte piece of a
 //    contiguous row;
 //  * with a workspace, one persistent workgroup per CU slot claims work items from an

@@ -107,7 +107,10 @@ def greedy_generate(model, input_ids: torch.Tensor, steps: int, *, cache: str = 
         if cache != "paged":
             raise ValueError("graph decode needs the paged cache")
         from .graph_decode import GraphDecoder
+        t0 = time.perf_counter()
         dec = GraphDecoder(model, pkv, nxt, T + steps)
+        _sync(dev)
+        graph_setup = time.perf_counter() - t0
         for _ in range(steps):
             _sync(dev)
             t0 = time.perf_counter()
@@ -126,6 +129,7 @@ def greedy_generate(model, input_ids: torch.Tensor, steps: int, *, cache: str = 
         step_times.append(time.perf_counter() - t0)
         tokens.append(nxt)
     decode_s = sum(step_times)
-    return {"ttft_s": ttft, "decode_step_times_s": step_times, "decode_total_s": decode_s,
+    extra = {"graph_setup_s": graph_setup} if graph else {}
+    return {**extra, "ttft_s": ttft, "decode_step_times_s": step_times, "decode_total_s": decode_s,
             "decode_tokens_per_s": (B * steps / decode_s) if decode_s > 0 else None,
             "tokens": torch.stack(tokens, dim=1), "first_logits": first_logits, "cache": pkv}
