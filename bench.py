@@ -361,6 +361,41 @@ def stream_read_ceiling(dev, nbytes: int = 4 << 30, reps: int = 20) -> dict:
     return {"gbs": nbytes / (ev / reps) / 1e9, "bytes": nbytes, "launches": reps}
 
 
+def machine_ceilings(dev) -> dict:
+    """Ceilings the prefill kernel is read against, measured in the same run: the dense bf16
+    matrix-core rate (``sa_mfma_rate``: register-operand 32x32x16 MFMAs, four independent chains per
+    wave) at two and four waves per SIMD, and the LDS rates of the prefill kernel's two fragment
+    reads (``sa_lds_read_rate``: 8 waves per CU, as the kernel runs) in bytes per ns per CU."""
+    import torch
+    from sparseattentioninfer_amd import _lib
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    cus = int(lib.sa_measure_cus())
+    out = {}
+    for per_cu in (2, 4):
+        iters = 16000
+        sink = torch.empty(256 * per_cu * cus, dtype=torch.float32, device=dev)
+
+        def launch():
+            _lib.check("sa_mfma_rate", lib.sa_mfma_rate(per_cu, iters, sink.data_ptr(), stream))
+
+        _, ev = _events_time(launch, 5, 2)
+        flop = 4 * iters * 32768 * 256 * per_cu * cus
+        out[f"mfma_bf16_tflops_{per_cu}_waves_per_simd"] = flop / (ev / 5) / 1e12
+    for tr16, key in ((0, "lds_ds_read_b128_bytes_per_ns_per_cu"), (1, "lds_ds_read_b64_tr_b16_bytes_per_ns_per_cu")):
+        iters = 4000
+        sink = torch.empty(512 * cus, dtype=torch.int32, device=dev)
+
+        def launch():
+            _lib.check("sa_lds_read_rate", lib.sa_lds_read_rate(tr16, iters, sink.data_ptr(), stream))
+
+        _, ev = _events_time(launch, 5, 2)
+        out[key] = 8 * 16384 * iters / (ev / 5) / 1e9
+    out["note"] = ("measured in this run; the published peaks (2.5 PFLOP/s bf16 at 2.4 GHz) assume a clock the "
+                   "boxes do not hold under sustained matrix load")
+    return out
+
+
 def _time_decode(args, dev, random_blocks: int):
     """Fastest of num_splits 1 and 2 (or the one asked for), timed cache-cold: DECODE_ROTATION
     workloads (over 1 GB of retained K/V per cycle, against a 256 MB Infinity Cache) launched in
@@ -697,7 +732,7 @@ def main():
         torch.cuda.empty_cache()
     if args.only == "all":
         line["leg_order"] = ("e2e, " if e2e_done is not None else "") + \
-            "configs[2] prefill, configs[1] prefill, decode, pattern build, cpu baseline"
+            "configs[2] prefill, machine ceilings, configs[1] prefill, decode, pattern build, cpu baseline"
     pre = None
     if args.only in ("all", "prefill"):
         pre = run_prefill(args, dev)
@@ -709,6 +744,10 @@ def main():
         line["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pre["roofline"].items()}
         ex = line["roofline"]["exact_causal"]
         line["roofline"]["exact_causal"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in ex.items()}
+        mach = machine_ceilings(dev)
+        line["machine"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in mach.items()}
+        ceiling = max(mach["mfma_bf16_tflops_2_waves_per_simd"], mach["mfma_bf16_tflops_4_waves_per_simd"])
+        line["roofline"]["frac_of_measured_mfma_ceiling"] = round(pre["roofline"]["achieved"] / ceiling, 4)
     if args.only in ("all", "bernoulli"):
         c1 = run_prefill_bernoulli(args, dev)
         c1["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c1["roofline"].items()}

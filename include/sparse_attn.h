@@ -277,6 +277,23 @@ int sa_stream_read(const void* src, int64_t bytes, uint32_t* sink, void* stream)
 int sa_stream_read_workgroups(void);
 
 /*
+ * Measurement aids, no counterpart in the reference: the ceilings the prefill
+ * kernel is read against.  sa_mfma_rate launches per_cu (1..8) 4-wave
+ * workgroups per CU (so per_cu waves per SIMD); every wave runs `iters` rounds
+ * of 4 independent v_mfma_f32_32x32x16_bf16 (32768 FLOP each) on register
+ * operands: 4 * iters * 32768 * 256 * per_cu * sa_measure_cus() FLOP per
+ * launch.  sink: that many floats per 256 threads (256 * per_cu * CUs floats).
+ * sa_lds_read_rate launches one 8-wave workgroup per CU; every wave reads a
+ * 16 KiB LDS tile `iters` times with the prefill kernel's K-fragment read
+ * (tr16 = 0: ds_read_b128) or V-fragment read (tr16 = 1: two
+ * ds_read_b64_tr_b16): 8 * 16384 * iters bytes per CU and launch.  sink: 512
+ * uint32 per CU.
+ */
+int sa_mfma_rate(int per_cu, int iters, float* sink, void* stream);
+int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, void* stream);
+int sa_measure_cus(void);
+
+/*
  * Fused elementwise stages of one decode step of a Qwen3 decoder layer, for the
  * graph-captured end-to-end decode (callers of the attention path, not the
  * attention itself).  They keep Hugging Face's arithmetic: fp32 inside,

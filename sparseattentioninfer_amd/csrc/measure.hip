@@ -1,7 +1,9 @@
-// Measurement aid: the HBM streaming-read rate of this GPU, the practical ceiling against which
-// the memory-bound decode kernel is read (bench.py reports both in the same run).  Not part of the
-// attention path.
+// Measurement aids: the HBM streaming-read rate of this GPU, the practical ceiling against which
+// the memory-bound decode kernel is read, and the dense bf16 matrix-core rate and LDS fragment-read
+// rates that bound the prefill kernel (bench.py reports them beside the kernels, in the same run).
+// Not part of the attention path.
 //
+// Streaming read:
 // A grid of 8 workgroups per CU; each workgroup reads one contiguous chunk of `src` (1/grid of
 // it) front to back, its 256 threads covering 4 KiB per load instruction, eight non-temporal
 // loads in flight, and folds the words with xor into one word per workgroup (written to
@@ -43,7 +45,124 @@ __global__ __launch_bounds__(SR_THREADS) void stream_read_kernel(const u32x4* sr
   }
 }
 
+// Dense matrix-core rate: every wave runs `iters` rounds of MR_CHAINS independent
+// v_mfma_f32_32x32x16_bf16 accumulations (32768 FLOP each) on register operands, and folds its
+// accumulators into sink[global thread] so nothing is dropped.  Launched with `per_cu` 4-wave
+// workgroups per CU, the SIMDs run `per_cu` waves each.
+constexpr int MR_THREADS = 256;
+constexpr int MR_CHAINS = 4;
+
+__global__ __launch_bounds__(MR_THREADS) void mfma_rate_kernel(int iters, float* sink) {
+  using E = Elem<true>;
+  const uint32_t t = threadIdx.x;
+  // small finite bf16 values, different per lane
+  const u32x4 a = {0x3c003c00u + t, 0x3c013c01u, 0x3c023c02u, 0x3c033c03u};
+  const u32x4 b = {0x3b003b00u + (t >> 1), 0x3b013b01u, 0x3b023b02u, 0x3b033b03u};
+  f32x16 acc[MR_CHAINS];
+#pragma unroll
+  for (int c = 0; c < MR_CHAINS; ++c) acc[c] = f32x16{};
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int c = 0; c < MR_CHAINS; ++c) acc[c] = E::mfma32(a, b, acc[c]);
+  }
+  float x = 0.f;
+#pragma unroll
+  for (int c = 0; c < MR_CHAINS; ++c)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) x += acc[c][e];
+  sink[(int64_t)blockIdx.x * MR_THREADS + t] = x;
+}
+
+// LDS fragment-read rate: one 8-wave workgroup per CU (two waves per SIMD, as the prefill kernel
+// runs) reads a 16 KiB staged tile `iters` times per wave with the prefill kernel's two fragment
+// reads: 16-byte ds_read_b128 (lane l: row l % 32, 16-byte chunk l / 32 of a 64-byte row, chunks
+// swizzled by (row / 4) % 4 as in the staged K tiles) or two 8-byte ds_read_b64_tr_b16 (the
+// transposing V^T read of four 16-bit keys); 16 reads per round, xor-folded into sink.
+constexpr int LR_THREADS = 512;
+constexpr int LR_TILE = 16384;
+
+__device__ __forceinline__ u32x2 lr_tr16(const char* p) {
+  typedef short v4i16 __attribute__((ext_vector_type(4)));
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4i16*)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+template <bool TR16>
+__global__ __launch_bounds__(LR_THREADS) void lds_rate_kernel(int iters, uint32_t* sink) {
+  __shared__ __attribute__((aligned(16))) char tile[LR_TILE];
+  const int t = threadIdx.x, lane = t & 63;
+  for (int x = t; x < LR_TILE / 4; x += LR_THREADS) reinterpret_cast<uint32_t*>(tile)[x] = 0x9e3779b9u * x;
+  __syncthreads();
+  const int l32 = lane & 31, g = lane >> 5;
+  const int k0 = l32 * 64 + 16 * (g ^ ((l32 >> 2) & 3));
+  const int i16 = lane & 15, G = lane >> 4;
+  const int c4 = 2 * (G & 1) + ((i16 >> 1) & 1);
+  const int v0 = (8 * g + (i16 >> 2)) * 64 + 16 * (c4 ^ (2 * g)) + 8 * (i16 & 1);
+  u32x4 acc = {0, 0, 0, 0};
+  for (int i = 0; i < iters; ++i) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      // 16 KiB per round: 4 column groups x 2 row halves x 2 chunk parities (b128), or
+      // 4 x 2 x 2 1 KiB blocks of two transposing reads each (tr16)
+      const char* p = tile + 4096 * (r & 3) + 2048 * ((r >> 2) & 1);
+      if constexpr (TR16) {
+        const char* q = p + 1024 * (r >> 3);
+        const u32x2 lo = lr_tr16(q + v0);
+        const u32x2 hi = lr_tr16(q + ((v0 + 256) ^ 16));
+        acc ^= u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        acc ^= *reinterpret_cast<const u32x4*>(p + ((r >> 3) ? (k0 ^ 32) : k0));
+      }
+    }
+    // keeps each round's reads from being merged across rounds
+    asm volatile("" : "+v"(acc));
+  }
+  sink[(int64_t)blockIdx.x * LR_THREADS + t] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+}
+
 }  // namespace sa
+
+extern "C" int sa_mfma_rate(int per_cu, int iters, float* sink, void* stream) {
+  using namespace sa;
+  clear_error();
+  if (per_cu < 1 || per_cu > 8 || iters < 1) return set_error(SA_E_SHAPE, "sa_mfma_rate: per_cu %d (1..8), iters %d", per_cu, iters);
+  if (!sink) return set_error(SA_E_NULL, "sa_mfma_rate: NULL sink");
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  hipLaunchKernelGGL(mfma_rate_kernel, dim3(cus * per_cu), dim3(MR_THREADS), 0, static_cast<hipStream_t>(stream),
+                     iters, sink);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_error((int)err, "sa_mfma_rate: launch failed: %s", hipGetErrorString(err));
+  return 0;
+}
+
+extern "C" int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, void* stream) {
+  using namespace sa;
+  clear_error();
+  if (iters < 1) return set_error(SA_E_SHAPE, "sa_lds_read_rate: iters %d", iters);
+  if (!sink) return set_error(SA_E_NULL, "sa_lds_read_rate: NULL sink");
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  if (tr16)
+    hipLaunchKernelGGL(lds_rate_kernel<true>, dim3(cus), dim3(LR_THREADS), 0, static_cast<hipStream_t>(stream), iters, sink);
+  else
+    hipLaunchKernelGGL(lds_rate_kernel<false>, dim3(cus), dim3(LR_THREADS), 0, static_cast<hipStream_t>(stream), iters, sink);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_error((int)err, "sa_lds_read_rate: launch failed: %s", hipGetErrorString(err));
+  return 0;
+}
+
+extern "C" int sa_measure_cus(void) {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    cus = 256;
+  return cus;
+}
 
 extern "C" int sa_stream_read_workgroups(void) {
   int dev = 0, cus = 0;
