@@ -380,7 +380,7 @@ def machine_ceilings(dev) -> dict:
             _lib.check("sa_mfma_rate", lib.sa_mfma_rate(per_cu, iters, sink.data_ptr(), stream))
 
         _, ev = _events_time(launch, 5, 2)
-        flop = 4 * iters * 32768 * 256 * per_cu * cus
+        flop = 4 * iters * 32768 * 4 * per_cu * cus   # 4 MFMAs per round, 4 waves per workgroup
         out[f"mfma_bf16_tflops_{per_cu}_waves_per_simd"] = flop / (ev / 5) / 1e12
     for tr16, key in ((0, "lds_ds_read_b128_bytes_per_ns_per_cu"), (1, "lds_ds_read_b64_tr_b16_bytes_per_ns_per_cu")):
         iters = 4000

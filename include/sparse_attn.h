@@ -281,8 +281,8 @@ int sa_stream_read_workgroups(void);
  * kernel is read against.  sa_mfma_rate launches per_cu (1..8) 4-wave
  * workgroups per CU (so per_cu waves per SIMD); every wave runs `iters` rounds
  * of 4 independent v_mfma_f32_32x32x16_bf16 (32768 FLOP each) on register
- * operands: 4 * iters * 32768 * 256 * per_cu * sa_measure_cus() FLOP per
- * launch.  sink: that many floats per 256 threads (256 * per_cu * CUs floats).
+ * operands: 4 * iters * 32768 * 4 * per_cu * sa_measure_cus() FLOP per
+ * launch (four waves per workgroup).  sink: that many floats per 256 threads (256 * per_cu * CUs floats).
  * sa_lds_read_rate launches one 8-wave workgroup per CU; every wave reads a
  * 16 KiB LDS tile `iters` times with the prefill kernel's K-fragment read
  * (tr16 = 0: ds_read_b128) or V-fragment read (tr16 = 1: two
