@@ -364,8 +364,9 @@ def stream_read_ceiling(dev, nbytes: int = 4 << 30, reps: int = 20) -> dict:
 def machine_ceilings(dev) -> dict:
     """Ceilings the prefill kernel is read against, measured in the same run: the dense bf16
     matrix-core rate (``sa_mfma_rate``: register-operand 32x32x16 MFMAs, four independent chains per
-    wave) at two and four waves per SIMD, and the LDS rates of the prefill kernel's two fragment
-    reads (``sa_lds_read_rate``: 8 waves per CU, as the kernel runs) in bytes per ns per CU."""
+    wave) at two and four waves per SIMD, sustained over about 0.1 s, and the LDS rates of the
+    prefill kernel's two fragment reads (``sa_lds_read_rate``: 8 waves per CU, as the kernel runs)
+    in bytes per ns per CU."""
     import torch
     from sparseattentioninfer_amd import _lib
     lib = _lib.load()
@@ -373,11 +374,12 @@ def machine_ceilings(dev) -> dict:
     cus = int(lib.sa_measure_cus())
     out = {}
     for per_cu in (2, 4):
-        iters = 16000
+        # about 20 ms per launch, so the rate is the one the clock sustains under matrix load
+        iters = 320000 // per_cu
         sink = torch.empty(256 * per_cu * cus, dtype=torch.float32, device=dev)
 
         def launch():
-            _lib.check("sa_mfma_rate", lib.sa_mfma_rate(per_cu, iters, sink.data_ptr(), stream))
+            _lib.check("sa_mfma_rate", lib.sa_mfma_rate(per_cu, iters, sink.data_ptr(), sink.numel(), stream))
 
         _, ev = _events_time(launch, 5, 2)
         flop = 4 * iters * 32768 * 4 * per_cu * cus   # 4 MFMAs per round, 4 waves per workgroup
@@ -387,7 +389,7 @@ def machine_ceilings(dev) -> dict:
         sink = torch.empty(512 * cus, dtype=torch.int32, device=dev)
 
         def launch():
-            _lib.check("sa_lds_read_rate", lib.sa_lds_read_rate(tr16, iters, sink.data_ptr(), stream))
+            _lib.check("sa_lds_read_rate", lib.sa_lds_read_rate(tr16, iters, sink.data_ptr(), sink.numel(), stream))
 
         _, ev = _events_time(launch, 5, 2)
         out[key] = 8 * 16384 * iters / (ev / 5) / 1e9

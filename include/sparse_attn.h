@@ -282,15 +282,16 @@ int sa_stream_read_workgroups(void);
  * workgroups per CU (so per_cu waves per SIMD); every wave runs `iters` rounds
  * of 4 independent v_mfma_f32_32x32x16_bf16 (32768 FLOP each) on register
  * operands: 4 * iters * 32768 * 4 * per_cu * sa_measure_cus() FLOP per
- * launch (four waves per workgroup).  sink: that many floats per 256 threads (256 * per_cu * CUs floats).
+ * launch (four waves per workgroup); each thread writes one float to sink,
+ * so sink_len >= 256 * per_cu * sa_measure_cus().
  * sa_lds_read_rate launches one 8-wave workgroup per CU; every wave reads a
  * 16 KiB LDS tile `iters` times with the prefill kernel's K-fragment read
  * (tr16 = 0: ds_read_b128) or V-fragment read (tr16 = 1: two
- * ds_read_b64_tr_b16): 8 * 16384 * iters bytes per CU and launch.  sink: 512
- * uint32 per CU.
+ * ds_read_b64_tr_b16): 8 * 16384 * iters bytes per CU and launch; sink_len >=
+ * 512 * sa_measure_cus() words.  A shorter sink is refused (SA_E_SHAPE).
  */
-int sa_mfma_rate(int per_cu, int iters, float* sink, void* stream);
-int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, void* stream);
+int sa_mfma_rate(int per_cu, int iters, float* sink, int64_t sink_len, void* stream);
+int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, int64_t sink_len, void* stream);
 int sa_measure_cus(void);
 
 /*

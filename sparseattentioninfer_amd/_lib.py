@@ -94,8 +94,8 @@ SIGNATURES = {
     "sa_decode_noalloc_scratch_bytes": (_i64, []),
     "sa_stream_read": (_i32, [_vp, _i64, _vp, _vp]),
     "sa_stream_read_workgroups": (_i32, []),
-    "sa_mfma_rate": (_i32, [_i32, _i32, _vp, _vp]),
-    "sa_lds_read_rate": (_i32, [_i32, _i32, _vp, _vp]),
+    "sa_mfma_rate": (_i32, [_i32, _i32, _vp, _i64, _vp]),
+    "sa_lds_read_rate": (_i32, [_i32, _i32, _vp, _i64, _vp]),
     "sa_measure_cus": (_i32, []),
     "sa_rmsnorm": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "sa_qk_rope_kv": (_i32, [

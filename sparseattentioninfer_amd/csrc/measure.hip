@@ -55,9 +55,19 @@ constexpr int MR_CHAINS = 4;
 __global__ __launch_bounds__(MR_THREADS) void mfma_rate_kernel(int iters, float* sink) {
   using E = Elem<true>;
   const uint32_t t = threadIdx.x;
-  // small finite bf16 values, different per lane
-  const u32x4 a = {0x3c003c00u + t, 0x3c013c01u, 0x3c023c02u, 0x3c033c03u};
-  const u32x4 b = {0x3b003b00u + (t >> 1), 0x3b013b01u, 0x3b023b02u, 0x3b033b03u};
+  const uint32_t seed = t + MR_THREADS * blockIdx.x;
+  // bf16 values in [0.5, 1) with hashed mantissas and signs, different per lane and element: the
+  // multipliers toggle as they do on attention data (operand bits set how much power, and so how
+  // much clock, the matrix cores draw)
+  auto h = [&](uint32_t k) {
+    uint32_t x = (seed + 1u) * 0x9e3779b9u ^ (k * 0x85ebca6bu);
+    x ^= x >> 15;
+    x *= 0x2c1b3c6du;
+    x ^= x >> 12;
+    return (x & 0x807f807fu) | 0x3f003f00u;
+  };
+  const u32x4 a = {h(0), h(1), h(2), h(3)};
+  const u32x4 b = {h(4), h(5), h(6), h(7)};
   f32x16 acc[MR_CHAINS];
 #pragma unroll
   for (int c = 0; c < MR_CHAINS; ++c) acc[c] = f32x16{};
@@ -122,15 +132,23 @@ __global__ __launch_bounds__(LR_THREADS) void lds_rate_kernel(int iters, uint32_
 
 }  // namespace sa
 
-extern "C" int sa_mfma_rate(int per_cu, int iters, float* sink, void* stream) {
-  using namespace sa;
-  clear_error();
-  if (per_cu < 1 || per_cu > 8 || iters < 1) return set_error(SA_E_SHAPE, "sa_mfma_rate: per_cu %d (1..8), iters %d", per_cu, iters);
-  if (!sink) return set_error(SA_E_NULL, "sa_mfma_rate: NULL sink");
+extern "C" int sa_measure_cus(void) {
   int dev = 0, cus = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
     cus = 256;
+  return cus;
+}
+
+extern "C" int sa_mfma_rate(int per_cu, int iters, float* sink, int64_t sink_len, void* stream) {
+  using namespace sa;
+  clear_error();
+  if (per_cu < 1 || per_cu > 8 || iters < 1) return set_error(SA_E_SHAPE, "sa_mfma_rate: per_cu %d (1..8), iters %d", per_cu, iters);
+  if (!sink) return set_error(SA_E_NULL, "sa_mfma_rate: NULL sink");
+  const int cus = sa_measure_cus();
+  if (sink_len < (int64_t)MR_THREADS * per_cu * cus)
+    return set_error(SA_E_SHAPE, "sa_mfma_rate: sink of %lld floats, needs %lld", (long long)sink_len,
+                     (long long)MR_THREADS * per_cu * cus);
   hipLaunchKernelGGL(mfma_rate_kernel, dim3(cus * per_cu), dim3(MR_THREADS), 0, static_cast<hipStream_t>(stream),
                      iters, sink);
   const hipError_t err = hipGetLastError();
@@ -138,15 +156,15 @@ extern "C" int sa_mfma_rate(int per_cu, int iters, float* sink, void* stream) {
   return 0;
 }
 
-extern "C" int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, void* stream) {
+extern "C" int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, int64_t sink_len, void* stream) {
   using namespace sa;
   clear_error();
   if (iters < 1) return set_error(SA_E_SHAPE, "sa_lds_read_rate: iters %d", iters);
   if (!sink) return set_error(SA_E_NULL, "sa_lds_read_rate: NULL sink");
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-    cus = 256;
+  const int cus = sa_measure_cus();
+  if (sink_len < (int64_t)LR_THREADS * cus)
+    return set_error(SA_E_SHAPE, "sa_lds_read_rate: sink of %lld words, needs %lld", (long long)sink_len,
+                     (long long)LR_THREADS * cus);
   if (tr16)
     hipLaunchKernelGGL(lds_rate_kernel<true>, dim3(cus), dim3(LR_THREADS), 0, static_cast<hipStream_t>(stream), iters, sink);
   else
@@ -154,14 +172,6 @@ extern "C" int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, void* strea
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return set_error((int)err, "sa_lds_read_rate: launch failed: %s", hipGetErrorString(err));
   return 0;
-}
-
-extern "C" int sa_measure_cus(void) {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-    cus = 256;
-  return cus;
 }
 
 extern "C" int sa_stream_read_workgroups(void) {

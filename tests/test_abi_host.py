@@ -86,9 +86,12 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
                                None, 8 * 16, 16, None, 16, 2, 8, None, 4096, 128, B, 32, 8, 128, 64, 0.088, 16, None)
     assert st == -7 and b"scratch bytes" in lib.sa_last_error()
     # measurement aids: shapes checked before any launch
-    assert lib.sa_mfma_rate(0, 10, None, None) != 0 and b"per_cu 0" in lib.sa_last_error()
-    assert lib.sa_mfma_rate(2, 10, None, None) != 0 and b"NULL sink" in lib.sa_last_error()
-    assert lib.sa_lds_read_rate(0, 0, None, None) != 0 and b"iters 0" in lib.sa_last_error()
+    assert lib.sa_mfma_rate(0, 10, None, 0, None) != 0 and b"per_cu 0" in lib.sa_last_error()
+    assert lib.sa_mfma_rate(2, 10, None, 0, None) != 0 and b"NULL sink" in lib.sa_last_error()
+    assert lib.sa_lds_read_rate(0, 0, None, 0, None) != 0 and b"iters 0" in lib.sa_last_error()
+    # a sink shorter than one word per launched thread is refused before the launch
+    assert lib.sa_mfma_rate(2, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
+    assert lib.sa_lds_read_rate(1, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

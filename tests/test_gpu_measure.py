@@ -36,14 +36,14 @@ def test_ceilings_are_plausible():
     _say(f"[measure] mfma rate, {cus} CUs")
     iters = 4000
     sink = torch.empty(256 * 2 * cus, dtype=torch.float32, device="cuda")
-    t = _time(lambda: _lib.check("sa_mfma_rate", lib.sa_mfma_rate(2, iters, sink.data_ptr(), stream)))
+    t = _time(lambda: _lib.check("sa_mfma_rate", lib.sa_mfma_rate(2, iters, sink.data_ptr(), sink.numel(), stream)))
     pflops = 4 * iters * 32768 * 4 * 2 * cus / t / 1e15   # 4 MFMAs per round, 4 waves per workgroup
     assert torch.isfinite(sink).all()
     assert 0.5 < pflops < 2.6, pflops        # the dense bf16 peak is 2.5 PFLOP/s at 2.4 GHz
     for tr16 in (0, 1):
         _say(f"[measure] lds rate tr16={tr16}")
         sink = torch.empty(512 * cus, dtype=torch.int32, device="cuda")
-        t = _time(lambda: _lib.check("sa_lds_read_rate", lib.sa_lds_read_rate(tr16, 1000, sink.data_ptr(), stream)))
+        t = _time(lambda: _lib.check("sa_lds_read_rate", lib.sa_lds_read_rate(tr16, 1000, sink.data_ptr(), sink.numel(), stream)))
         per_cu = 8 * 16384 * 1000 / t / 1e9     # bytes per ns per CU
         assert 50 < per_cu < 1000, per_cu       # at most 256 B per clock at 2.4 GHz is 614 B/ns
     _say("[measure] stream read")
