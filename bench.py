@@ -364,9 +364,10 @@ def stream_read_ceiling(dev, nbytes: int = 4 << 30, reps: int = 20) -> dict:
 def machine_ceilings(dev) -> dict:
     """Ceilings the prefill kernel is read against, measured in the same run: the dense bf16
     matrix-core rate (``sa_mfma_rate``: register-operand 32x32x16 MFMAs, four independent chains per
-    wave) at two and four waves per SIMD, sustained over about 0.1 s, and the LDS rates of the
+    wave) at two and four waves per SIMD, sustained over about 0.1 s, the LDS rates of the
     prefill kernel's two fragment reads (``sa_lds_read_rate``: 8 waves per CU, as the kernel runs)
-    in bytes per ns per CU."""
+    and the per-CU rate of its tile staging (``sa_stage_rate``: direct loads of L2-resident 16 KiB
+    tiles, a barrier per tile), in bytes per ns per CU."""
     import torch
     from sparseattentioninfer_amd import _lib
     lib = _lib.load()
@@ -393,6 +394,16 @@ def machine_ceilings(dev) -> dict:
 
         _, ev = _events_time(launch, 5, 2)
         out[key] = 8 * 16384 * iters / (ev / 5) / 1e9
+    src = torch.ones(1 << 16, dtype=torch.uint8, device=dev)
+    sink = torch.empty(512 * cus, dtype=torch.int32, device=dev)
+    iters = 20000
+
+    def launch():
+        _lib.check("sa_stage_rate", lib.sa_stage_rate(src.data_ptr(), src.numel(), iters, sink.data_ptr(),
+                                                      sink.numel(), stream))
+
+    _, ev = _events_time(launch, 5, 2)
+    out["staging_direct_load_bytes_per_ns_per_cu"] = 16384 * iters / (ev / 5) / 1e9
     out["note"] = ("measured in this run; the published peaks (2.5 PFLOP/s bf16 at 2.4 GHz) assume a clock the "
                    "boxes do not hold under sustained matrix load")
     return out

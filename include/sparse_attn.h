@@ -295,6 +295,17 @@ int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, int64_t sink_len, void
 int sa_measure_cus(void);
 
 /*
+ * Measurement aid, no counterpart in the reference: the per-CU rate of the
+ * load path that stages the prefill kernel's K/V tiles.  One 8-wave workgroup
+ * per CU moves a 16 KiB tile of src (L2-resident: 4 tiles in turn, so
+ * src_bytes >= 65536, 16-byte aligned) into LDS with direct loads
+ * (global_load_lds_dwordx4), waits and meets at a barrier, `iters` times:
+ * 16384 * iters bytes per CU and launch.  sink_len >= 512 * sa_measure_cus()
+ * words.
+ */
+int sa_stage_rate(const void* src, int64_t src_bytes, int iters, uint32_t* sink, int64_t sink_len, void* stream);
+
+/*
  * Fused elementwise stages of one decode step of a Qwen3 decoder layer, for the
  * graph-captured end-to-end decode (callers of the attention path, not the
  * attention itself).  They keep Hugging Face's arithmetic: fp32 inside,

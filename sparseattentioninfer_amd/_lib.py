@@ -97,6 +97,7 @@ SIGNATURES = {
     "sa_mfma_rate": (_i32, [_i32, _i32, _vp, _i64, _vp]),
     "sa_lds_read_rate": (_i32, [_i32, _i32, _vp, _i64, _vp]),
     "sa_measure_cus": (_i32, []),
+    "sa_stage_rate": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp]),
     "sa_rmsnorm": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "sa_qk_rope_kv": (_i32, [
         _i32, _vp, _i64, _vp, _vp, _vp, _vp,

@@ -130,6 +130,36 @@ __global__ __launch_bounds__(LR_THREADS) void lds_rate_kernel(int iters, uint32_
   sink[(int64_t)blockIdx.x * LR_THREADS + t] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
+// Staging rate: one 8-wave workgroup per CU moves 16 KiB tiles of an L2-resident source into LDS
+// with the prefill kernel's direct loads (global_load_lds_dwordx4, two 1 KiB loads per wave and
+// tile), waits for them and meets at a barrier, `iters` times: the per-CU rate of the load path
+// that stages K/V tiles (and Q) in the prefill kernel.  src: at least 64 KiB, 16-byte aligned;
+// tiles rotate over it.
+constexpr int ST_THREADS = 512;
+
+__global__ __launch_bounds__(ST_THREADS) void stage_rate_kernel(const char* src, int iters, uint32_t* sink) {
+  __shared__ __attribute__((aligned(16))) char tile[2 * LR_TILE];
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const uint32_t voff = 16u * lane;
+  for (int i = 0; i < iters; ++i) {
+    const char* s = src + (int64_t)(i & 3) * LR_TILE;  // 4 tiles of the 64 KiB source in turn
+    char* d = tile + (i & 1) * LR_TILE;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int k = 2 * wave + u;  // 1 KiB piece k of the 16 KiB tile
+      const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(d + 1024 * k);
+      asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                   :
+                   : "v"(voff), "s"(s + 1024 * k), "s"(lds)
+                   : "memory", "m0");
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+  }
+  sink[(int64_t)blockIdx.x * ST_THREADS + t] = reinterpret_cast<const uint32_t*>(tile)[t];
+}
+
 }  // namespace sa
 
 extern "C" int sa_measure_cus(void) {
@@ -171,6 +201,25 @@ extern "C" int sa_lds_read_rate(int tr16, int iters, uint32_t* sink, int64_t sin
     hipLaunchKernelGGL(lds_rate_kernel<false>, dim3(cus), dim3(LR_THREADS), 0, static_cast<hipStream_t>(stream), iters, sink);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) return set_error((int)err, "sa_lds_read_rate: launch failed: %s", hipGetErrorString(err));
+  return 0;
+}
+
+extern "C" int sa_stage_rate(const void* src, int64_t src_bytes, int iters, uint32_t* sink, int64_t sink_len,
+                             void* stream) {
+  using namespace sa;
+  clear_error();
+  if (iters < 1) return set_error(SA_E_SHAPE, "sa_stage_rate: iters %d", iters);
+  if (!src || !sink) return set_error(SA_E_NULL, "sa_stage_rate: NULL pointer");
+  if (src_bytes < 4 * LR_TILE) return set_error(SA_E_SHAPE, "sa_stage_rate: src of %lld bytes, needs %d", (long long)src_bytes, 4 * LR_TILE);
+  if (reinterpret_cast<uintptr_t>(src) & 15) return set_error(SA_E_ALIGN, "sa_stage_rate: src must be 16-byte aligned");
+  const int cus = sa_measure_cus();
+  if (sink_len < (int64_t)ST_THREADS * cus)
+    return set_error(SA_E_SHAPE, "sa_stage_rate: sink of %lld words, needs %lld", (long long)sink_len,
+                     (long long)ST_THREADS * cus);
+  hipLaunchKernelGGL(stage_rate_kernel, dim3(cus), dim3(ST_THREADS), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const char*>(src), iters, sink);
+  const hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return set_error((int)err, "sa_stage_rate: launch failed: %s", hipGetErrorString(err));
   return 0;
 }
 

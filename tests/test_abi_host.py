@@ -92,6 +92,8 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     # a sink shorter than one word per launched thread is refused before the launch
     assert lib.sa_mfma_rate(2, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
     assert lib.sa_lds_read_rate(1, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
+    assert lib.sa_stage_rate(fake, 1024, 10, fake, 1 << 20, None) != 0 and b"needs 65536" in lib.sa_last_error()
+    assert lib.sa_stage_rate(fake, 1 << 16, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

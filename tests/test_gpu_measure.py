@@ -46,6 +46,14 @@ def test_ceilings_are_plausible():
         t = _time(lambda: _lib.check("sa_lds_read_rate", lib.sa_lds_read_rate(tr16, 1000, sink.data_ptr(), sink.numel(), stream)))
         per_cu = 8 * 16384 * 1000 / t / 1e9     # bytes per ns per CU
         assert 50 < per_cu < 1000, per_cu       # at most 256 B per clock at 2.4 GHz is 614 B/ns
+    _say("[measure] staging rate")
+    src = torch.ones(1 << 16, dtype=torch.uint8, device="cuda")
+    sink = torch.empty(512 * cus, dtype=torch.int32, device="cuda")
+    t = _time(lambda: _lib.check("sa_stage_rate", lib.sa_stage_rate(src.data_ptr(), src.numel(), 2000, sink.data_ptr(),
+                                                                     sink.numel(), stream)))
+    per_cu = 16384 * 2000 / t / 1e9
+    assert 5 < per_cu < 400, per_cu             # bytes per ns per CU
+    assert (sink == 0x01010101).all()           # the tile landed in LDS
     _say("[measure] stream read")
     n = 1 << 28
     buf = torch.ones(n, dtype=torch.uint8, device="cuda")
