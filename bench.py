@@ -180,6 +180,20 @@ def exact_causal_flops(bm, heads_per_row: int, D: int, batch: int = 1) -> int:
     return int(visible) * heads_per_row * batch * 4 * D
 
 
+def prefill_timeline(sets, pairs, offsets, launches: int = 12) -> dict:
+    """Per-phase timeline of the persistent prefill kernel (``sa_prefill_timeline``: an instrumented
+    copy of the kernel, run after the timed launches): the q/k/v sets launched in turn, and the last
+    launch of the first set summarized (shader clock, clocks per item phase, loop clocks per step,
+    workgroup start/end spread)."""
+    import torch
+    from sparseattentioninfer_amd import ops
+    tl = [ops.prepare_prefill_timeline(q, k, v, pairs, offsets, BS) for (q, k, v) in sets]
+    for i in range(launches):
+        tl[(i + 1) % len(tl)]()          # ends on set 0
+    torch.cuda.synchronize()
+    return ops.summarize_prefill_timeline(tl[0].timeline)
+
+
 def run_prefill(args, dev):
     import torch
     from sparseattentioninfer_amd import ops
@@ -191,6 +205,7 @@ def run_prefill(args, dev):
     wall, ev = _events_time(launch, args.steps, args.warmup)
     _, ev_one = _events_time(launches[0], args.steps, args.warmup)
     avg = ev / args.steps
+    timeline = prefill_timeline(sets, pairs, offsets)
     q, k, v = sets[0]
     info = {**info, "timing": f"{PREFILL_ROTATION} independent q/k/v sets launched in turn",
             "kernel_us_one_set_repeated": round(ev_one / args.steps * 1e6, 2),
@@ -210,6 +225,7 @@ def run_prefill(args, dev):
                                       "note": "secondary count: retained blocks with the masked upper triangle "
                                               "of each diagonal block removed"}},
         "tensors": (q, k, v, bm),
+        "timeline": timeline,
     }
     return res
 
@@ -255,6 +271,7 @@ def run_prefill_bernoulli(args, dev):
     wall, ev = _events_time(launch, args.steps, args.warmup)
     _, ev_one = _events_time(launches[0], args.steps, args.warmup)
     avg = ev / args.steps
+    timeline = prefill_timeline(sets, pairs, offsets)
     q, k, v = sets[0]
     return {**info, "timing": f"{PREFILL_ROTATION} independent q/k/v sets launched in turn",
             "kernel_us_one_set_repeated": round(ev_one / args.steps * 1e6, 2),
@@ -262,7 +279,7 @@ def run_prefill_bernoulli(args, dev):
             "kernel_us": avg * 1e6, "tflops": flops / (wall / args.steps) / 1e12, "flops_per_launch": flops,
             "roofline": {"bound": "mfma", "achieved": flops / avg / 1e12, "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": flops / avg / 1e12 / PEAK_BF16_TFLOPS, "traffic": None},
-            "tensors": (q, k, v, bm)}
+            "tensors": (q, k, v, bm), "timeline": timeline}
 
 
 def run_pattern_build(dev, reps: int = 20):
@@ -712,6 +729,13 @@ def _kernel_source_digest() -> dict:
     return out
 
 
+TIMELINE_NOTE = ("sa_prefill_timeline, an instrumented copy of the persistent prefill kernel launched after each "
+                 "prefill leg's timed launches (its own stamps cost about 100 clocks each): shader clocks "
+                 "(s_memtime) per item and phase for the first wave of each 32-row half, loop clocks per step, "
+                 "the shader clock against the 100 MHz s_memrealtime, and workgroup start/end times from the "
+                 "first workgroup start")
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -761,10 +785,13 @@ def main():
         line["machine"] = {k: (round(v, 2) if isinstance(v, float) else v) for k, v in mach.items()}
         ceiling = max(mach["mfma_bf16_tflops_2_waves_per_simd"], mach["mfma_bf16_tflops_4_waves_per_simd"])
         line["roofline"]["frac_of_measured_mfma_ceiling"] = round(pre["roofline"]["achieved"] / ceiling, 4)
+        line["prefill_timeline"] = {"note": TIMELINE_NOTE, "configs2": pre["timeline"]}
     if args.only in ("all", "bernoulli"):
         c1 = run_prefill_bernoulli(args, dev)
         c1["roofline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in c1["roofline"].items()}
-        line["configs1"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c1.items() if k != "tensors"}
+        line["configs1"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in c1.items()
+                            if k not in ("tensors", "timeline")}
+        line.setdefault("prefill_timeline", {"note": TIMELINE_NOTE})["configs1"] = c1["timeline"]
         if not args.no_cpu_baseline and args.only == "all":
             cb1 = cpu_baseline(c1, args.cpu_seconds / 3, "configs[1]")
             cb1["value"] = round(cb1["value"], 5)

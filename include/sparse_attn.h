@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 5
+#define SA_ABI_VERSION 6
 
 /* element types */
 #define SA_DTYPE_BF16 0
@@ -304,6 +304,39 @@ int sa_measure_cus(void);
  * words.
  */
 int sa_stage_rate(const void* src, int64_t src_bytes, int iters, uint32_t* sink, int64_t sink_len, void* stream);
+
+/*
+ * Measurement aid, no counterpart in the reference: sa_prefill (block size 64
+ * or 128, so no tile masks) through an instrumented copy of the persistent
+ * four-head kernel, which also writes a per-workgroup timeline.  Needs what
+ * that kernel needs: a workspace, Hq / csr_rows a multiple of four (four query
+ * heads per workgroup) and D = 128; other shapes are refused (SA_E_SHAPE).  The output
+ * o is the same as sa_prefill's.  timeline receives, for each workgroup w of the
+ * launch, 36 words at timeline[36 * w]: start and end in shader clocks
+ * (s_memtime) and in the 100 MHz constant clock (s_memrealtime); then for the
+ * first wave of the lower and of the upper 32-row half, 16 words each: the
+ * shader clocks spent in the phases of its items (0 gap before an item,
+ * 1 setup and Q load issue, 2 first tile-queue pops, 3 first K/V load issue,
+ * 4 lookahead issue, 5 load wait, 6 barrier, 7 first S^T, 8 tile loop, 9 last
+ * tile, 10 epilogue; 11 unused) and counts (12 items, 13 loop steps, 14 row
+ * reference refits; 15 the last stamp).  Each stamp costs about 100 shader
+ * clocks of its own.  timeline_words >= sa_prefill_timeline_words(dtype), the
+ * size for the largest grid on the current device.
+ */
+int sa_prefill_timeline(int dtype,
+                        const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                        const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                        const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                        void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                        const int32_t* pairs, int64_t pairs_stride,
+                        const int32_t* offsets, int64_t offsets_stride,
+                        int csr_rows, int nqb,
+                        int B, int Hq, int Hkv, int T_q, int T_k, int D,
+                        int block_size, int q_offset, float sm_scale,
+                        void* workspace, int64_t workspace_bytes,
+                        uint64_t* timeline, int64_t timeline_words,
+                        void* stream);
+int64_t sa_prefill_timeline_words(int dtype);
 
 /*
  * Fused elementwise stages of one decode step of a Qwen3 decoder layer, for the

@@ -11,7 +11,7 @@ import os
 import threading
 from pathlib import Path
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 DTYPE_BF16 = 0
 DTYPE_F16 = 1
 
@@ -98,6 +98,22 @@ SIGNATURES = {
     "sa_lds_read_rate": (_i32, [_i32, _i32, _vp, _i64, _vp]),
     "sa_measure_cus": (_i32, []),
     "sa_stage_rate": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp]),
+    "sa_prefill_timeline": (_i32, [
+        _i32,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64,
+        _vp, _i64,
+        _i32, _i32,
+        _i32, _i32, _i32, _i32, _i32, _i32,
+        _i32, _i32, _f32,
+        _vp, _i64,
+        _vp, _i64,
+        _vp,
+    ]),
+    "sa_prefill_timeline_words": (_i64, [_i32]),
     "sa_rmsnorm": (_i32, [_i32, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i32, _i32, _f32, _vp]),
     "sa_qk_rope_kv": (_i32, [
         _i32, _vp, _i64, _vp, _vp, _vp, _vp,

@@ -99,6 +99,8 @@ struct PrefillArgs {
   int nqb;
   int q_split, head_items, per_group, bhs;
   uint32_t mul_group, mul_bhs;
+  // Timeline launches only (sa_prefill_timeline): TL_WORDS words per workgroup.
+  unsigned long long* timeline;
 };
 
 // Words of the persistent-launch workspace: the next unclaimed item, the workgroups done, the
@@ -112,6 +114,33 @@ constexpr unsigned WS_SKIPPED = 1u;
 // CSR rows of a persistent launch in descending order of retained blocks (row_order).
 constexpr int MAX_ORDERED_ROWS = 256;
 __shared__ int s_row_rank[MAX_ORDERED_ROWS];
+
+// Timeline instantiation (TL) of the persistent four-head loop: shader-clock cycles (s_memtime)
+// spent in each phase of an item, summed over the workgroup's items, for the first wave of each
+// 32-row half; plus counts of items, loop steps and refits.  Each stamp costs about 100 cycles of
+// its own, so the instrumented launch runs a little slower than the product's.  Per workgroup
+// the record holds TL_WORDS words: start and end in shader clocks and in the 100 MHz constant
+// clock (s_memrealtime), then the 16 words of the lower half and the 16 of the upper half.
+enum : int {
+  TL_GAP = 0,        // end of the previous item (or workgroup start) to this item's setup
+  TL_SETUP_Q = 1,    // item setup and the Q load issue
+  TL_POPS = 2,       // tile queue start and the first two pops
+  TL_KV = 3,         // direct loads of the first K/V tiles issued
+  TL_LOOK = 4,       // lookahead reads and the next claim issued
+  TL_WAIT = 5,       // wait for every load, lookahead committed to LDS
+  TL_BARRIER = 6,    // the barrier that publishes the first tiles
+  TL_FIRST_QK = 7,   // Q fragments, the first tile's S^T and row max, the second barrier
+  TL_LOOP = 8,       // the tile loop (every step but the last tile's)
+  TL_LAST = 9,       // the last tile's probabilities and PV
+  TL_EPILOGUE = 10,  // normalisation, O staged and stored
+  TL_ITEMS = 12,     // counts: items,
+  TL_STEPS = 13,     // loop steps,
+  TL_REFITS = 14,    // refits of the row reference
+  TL_NOW = 15,       // (last stamp)
+  TL_HALF_WORDS = 16,
+  TL_WORDS = 4 + 2 * TL_HALF_WORDS
+};
+__shared__ unsigned s_tl[2][TL_HALF_WORDS];
 
 // Sum / max of a value over lanes l and l ^ 32, in every lane: one v_permlane32_swap of the
 // value with itself puts the lower half's values in one result and the upper half's in the other.
@@ -215,8 +244,8 @@ __device__ __forceinline__ int32_t load_lane_now(const int32_t* p) {
 }
 
 // SUB: tile schedules with sub-block masks (block sizes 16 and 32); without it the mask
-// bookkeeping compiles away.
-template <bool BF16, int D, int HW, bool SUB>
+// bookkeeping compiles away.  TL: the timeline instantiation (stamps compile away without it).
+template <bool BF16, int D, int HW, bool SUB, bool TL = false>
 struct Prefill {
   using E = Elem<BF16>;
   static constexpr int NW = 2 * HW;              // waves: HW query heads x two 32-row halves
@@ -240,6 +269,27 @@ struct Prefill {
   static constexpr float REFIT_SUM = 65536.f;
   static_assert(NI % NW == 0, "direct loads must split evenly over the waves");
   static_assert(NW * WAVE_BYTES <= LDS_KV, "the epilogue stages O in the K/V buffers");
+  static_assert(!TL || PIPE, "the timeline instruments the persistent four-head loop");
+
+  // TL only: charge the cycles since the last stamp to phase k (lane 0 of the first wave of each half).
+  static __device__ __forceinline__ void tl_stamp(int k) {
+    if constexpr (TL) {
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+      if (wave % HW == 0 && (threadIdx.x & 63) == 0) {
+        const unsigned t = (unsigned)__builtin_amdgcn_s_memtime();
+        unsigned* p = s_tl[wave / HW];
+        p[k] += t - p[TL_NOW];
+        p[TL_NOW] = t;
+      }
+    }
+  }
+  // TL only: count one event of kind k.
+  static __device__ __forceinline__ void tl_count(int k) {
+    if constexpr (TL) {
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+      if (wave % HW == 0 && (threadIdx.x & 63) == 0) s_tl[wave / HW][k] += 1;
+    }
+  }
 
   // LDS row of key k within a staged K tile: bits 2 and 3 swapped.  With this order the S^T
   // accumulator gives each lane half 8 consecutive keys per 16-key chunk, the k-order of the
@@ -889,9 +939,11 @@ struct Prefill {
     char* sV = sKV + NBK * TILE_BYTES;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    tl_stamp(TL_GAP);
     const Item it = LOOK ? setup_base(a, qt, r, hs, b, lk->e0, lk->n_ent) : setup(a, qt, r, hs, b, s_row, s_mask);
     char* sQw = sQ + wave * WAVE_BYTES;
     load_q(a, it.qb, it.q_row0, sQw, lane);  // Q^T operand of this wave into LDS
+    tl_stamp(TL_SETUP_Q);
     const Frag f(lane);
     const DmaLane dl(a, lane);
     // lim of tile kt: min(q_abs, T_k - 1) - kt*KT - 8g (past the tile when no key is masked)
@@ -934,16 +986,21 @@ struct Prefill {
     uint32_t m_cur = 0u, m_nxt = 0u;
     bool has_cur = queue_pop(a, it, s_row, s_mask, q, kt_cur, m_cur);
     bool has_nxt = has_cur && queue_pop(a, it, s_row, s_mask, q, kt_nxt, m_nxt);
+    tl_stamp(TL_POPS);
     if (has_cur) {
       load_k(kt_cur, 0);
       load_v(kt_cur, vb_first);
     }
     if (has_nxt) load_k(kt_nxt, 1);
+    tl_stamp(TL_KV);
     LookLoads ld;
     if constexpr (LOOK) look_issue(a, *lk, ld);
+    tl_stamp(TL_LOOK);
     wait_dma();
     if constexpr (LOOK) look_commit(*lk, ld);
+    tl_stamp(TL_WAIT);
     __syncthreads();
+    tl_stamp(TL_BARRIER);
     u32x4 Qr[D / 16];
 #pragma unroll
     for (int cc = 0; cc < D / 16; ++cc) Qr[cc] = qfrag(sQw, f, cc);
@@ -963,6 +1020,7 @@ struct Prefill {
     bool ref_ok = !__any(m_ref == -__builtin_inff());  // every row of the wave has a reference
     // The first step loads K of tile t2 into the buffer of t0, which the prime just read.
     __syncthreads();
+    tl_stamp(TL_FIRST_QK);
 
     // Each step holds two half-steps per wave: A = S^T of the next tile on the matrix cores
     // under the exponentials of this tile, B = O^T += V^T P^T of a tile under the row max of
@@ -1019,6 +1077,7 @@ struct Prefill {
     // O and l to it and recomputes the tile's probabilities.  Any reference gives the same result
     // up to rounding; the refit only keeps 2^(s c - m_ref) finite.
     auto refit = [&](const f32x16 (&Sc)[2], float& ls) {
+      tl_count(TL_REFITS);
       float mx = Sc[0][0];
 #pragma unroll
       for (int rr = 1; rr < 16; ++rr) mx = fmaxf(mx, Sc[0][rr]);
@@ -1112,6 +1171,7 @@ struct Prefill {
 
       wait_dma();
       __syncthreads();
+      tl_count(TL_STEPS);
       has_cur = has_nxt;
       kt_cur = kt_nxt;
       has_nxt = has_nn;
@@ -1159,13 +1219,17 @@ struct Prefill {
         S[0] = Sn[0];
         S[1] = Sn[1];
       }
+      tl_stamp(TL_LOOP);
       last_step(S);
       // Upper half: PV of the last tile.
       if (lag) block_pv(sV + vb_cur * TILE_BYTES);
       vb_first = vb_cur == 2 ? 0 : vb_cur + 1;  // read by neither half in the last step
     }
+    tl_stamp(TL_LAST);
     // O is staged in the wave's own Q slot (Q is in registers): no other wave touches it.
     epilogue(a, it, b, O, l_run, sQw, lane);
+    tl_stamp(TL_EPILOGUE);
+    tl_count(TL_ITEMS);
   }
 
   // Item index -> (qt, r, hs, b).  Per lane: v may differ between lanes (the startup reads two
@@ -1350,10 +1414,30 @@ struct Prefill {
 
     // Persistent: claim items from a counter until none is left.  The last workgroup to
     // finish resets the counter pair to zero for the next launch on the stream.
+    unsigned long long* rec = nullptr;  // TL: this workgroup's record
+    if constexpr (TL) {
+      rec = a.timeline + (int64_t)blockIdx.x * TL_WORDS;
+      if (threadIdx.x == 0) {
+        rec[0] = __builtin_amdgcn_s_memtime();
+        rec[1] = __builtin_amdgcn_s_memrealtime();
+      }
+      if (threadIdx.x < 2 * TL_HALF_WORDS) s_tl[threadIdx.x / TL_HALF_WORDS][threadIdx.x % TL_HALF_WORDS] = 0;
+      __syncthreads();
+      const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+      if (wave % HW == 0 && (threadIdx.x & 63) == 0) s_tl[wave / HW][TL_NOW] = (unsigned)__builtin_amdgcn_s_memtime();
+    }
     if (a.row_order) rank_rows(a, reinterpret_cast<int*>(sKV));  // K/V buffers are free here
     int done = 0;
     if constexpr (PIPE) {
       done = run_lookahead(a, n_items, sKV, sQ, s_row, s_mask);
+      if constexpr (TL) {
+        __syncthreads();  // every stamp is in LDS
+        if (threadIdx.x == 0) {
+          rec[2] = __builtin_amdgcn_s_memtime();
+          rec[3] = __builtin_amdgcn_s_memrealtime();
+        }
+        if (threadIdx.x < 2 * TL_HALF_WORDS) rec[4 + threadIdx.x] = s_tl[threadIdx.x / TL_HALF_WORDS][threadIdx.x % TL_HALF_WORDS];
+      }
     } else {
       for (;;) {
         if (threadIdx.x == 0) s_item = (int)atomicAdd(&a.counter[WS_NEXT], 1u);
@@ -1386,6 +1470,13 @@ template <bool BF16, int D, int HW, bool SUB>
 __global__ __launch_bounds__(128 * HW) __attribute__((amdgpu_waves_per_eu(2)))
 void prefill_kernel(PrefillArgs a) {
   Prefill<BF16, D, HW, SUB>::run(a);
+}
+
+// The timeline instantiation of the persistent four-head kernel (head dim 128, blocks of 64 or 128).
+template <bool BF16>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2)))
+void prefill_timeline_kernel(PrefillArgs a) {
+  Prefill<BF16, 128, 4, false, true>::run(a);
 }
 
 // Resident workgroups of one kernel instance per CU, and CUs, cached per device.
@@ -1440,53 +1531,60 @@ static hipError_t launch_d(const PrefillArgs& a, int hw, int64_t n_items, int64_
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-}  // namespace sa
+// Workgroups of a timeline launch on the current device: one per resident slot.
+static int64_t timeline_grid(bool bf16) {
+  int n = 0;
+  const hipError_t e = bf16 ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_timeline_kernel<true>, 512, 0)
+                            : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, prefill_timeline_kernel<false>, 512, 0);
+  if (e != hipSuccess || n < 1) n = 1;
+  return (int64_t)num_cus() * n;
+}
 
-extern "C" int sa_prefill(int dtype,
-                          const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
-                          const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
-                          const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
-                          void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
-                          const int32_t* pairs, int64_t pairs_stride,
-                          const int32_t* offsets, int64_t offsets_stride,
-                          const int32_t* tile_masks, int64_t tile_masks_stride,
-                          int csr_rows, int nqb,
-                          int B, int Hq, int Hkv, int T_q, int T_k, int D,
-                          int block_size, int q_offset, float sm_scale,
-                          void* workspace, int64_t workspace_bytes,
-                          void* stream) {
-  using namespace sa;
+static int prefill_impl(const char* fn, int dtype,
+                        const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                        const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                        const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                        void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                        const int32_t* pairs, int64_t pairs_stride,
+                        const int32_t* offsets, int64_t offsets_stride,
+                        const int32_t* tile_masks, int64_t tile_masks_stride,
+                        int csr_rows, int nqb,
+                        int B, int Hq, int Hkv, int T_q, int T_k, int D,
+                        int block_size, int q_offset, float sm_scale,
+                        void* workspace, int64_t workspace_bytes,
+                        void* stream,
+                        unsigned long long* timeline, int64_t timeline_words) {
   clear_error();
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F16)
-    return set_error(SA_E_DTYPE, "sa_prefill: dtype %d is not bf16 (0) or f16 (1)", dtype);
+    return set_error(SA_E_DTYPE, "%s: dtype %d is not bf16 (0) or f16 (1)", fn, dtype);
   if (B < 0 || Hq < 1 || Hkv < 1 || T_q < 0 || T_k < 0)
-    return set_error(SA_E_SHAPE, "sa_prefill: bad sizes B=%d Hq=%d Hkv=%d T_q=%d T_k=%d", B, Hq, Hkv, T_q, T_k);
+    return set_error(SA_E_SHAPE, "%s: bad sizes B=%d Hq=%d Hkv=%d T_q=%d T_k=%d", fn, B, Hq, Hkv, T_q, T_k);
   if (Hq % Hkv)
-    return set_error(SA_E_SHAPE, "sa_prefill: Hq=%d is not a multiple of Hkv=%d", Hq, Hkv);
+    return set_error(SA_E_SHAPE, "%s: Hq=%d is not a multiple of Hkv=%d", fn, Hq, Hkv);
   if (D != 64 && D != 128)
-    return set_error(SA_E_HEADDIM, "sa_prefill: head dim %d not supported (64, 128)", D);
+    return set_error(SA_E_HEADDIM, "%s: head dim %d not supported (64, 128)", fn, D);
   if (block_size != 16 && block_size != 32 && block_size != 64 && block_size != 128)
-    return set_error(SA_E_BLOCK, "sa_prefill: block size %d not supported (16, 32, 64, 128)", block_size);
+    return set_error(SA_E_BLOCK, "%s: block size %d not supported (16, 32, 64, 128)", fn, block_size);
   const bool tiled = block_size < 64;  // schedule of 64 x 64 tiles with sub-block masks
   if (tiled != (tile_masks != nullptr))
-    return set_error(SA_E_BLOCK, "sa_prefill: block size %d %s tile masks", block_size,
+    return set_error(SA_E_BLOCK, "%s: block size %d %s tile masks", fn, block_size,
                      tiled ? "needs" : "takes no");
   if (csr_rows != Hq && csr_rows != Hkv)
-    return set_error(SA_E_CSR, "sa_prefill: csr_rows=%d must be Hq=%d or Hkv=%d", csr_rows, Hq, Hkv);
+    return set_error(SA_E_CSR, "%s: csr_rows=%d must be Hq=%d or Hkv=%d", fn, csr_rows, Hq, Hkv);
   const int row_block = tiled ? 64 : block_size;  // query rows per CSR query block
   if (nqb != (int)ceil_div(T_q, row_block))
-    return set_error(SA_E_SHAPE, "sa_prefill: nqb=%d but ceil(T_q/%d)=%lld", nqb, row_block,
+    return set_error(SA_E_SHAPE, "%s: nqb=%d but ceil(T_q/%d)=%lld", fn, nqb, row_block,
                      (long long)ceil_div(T_q, row_block));
   if (B == 0 || T_q == 0) return 0;
   if (!q || !k || !v || !o || !pairs || !offsets)
-    return set_error(SA_E_NULL, "sa_prefill: NULL tensor pointer");
+    return set_error(SA_E_NULL, "%s: NULL tensor pointer", fn);
   const int64_t strides[] = {q_sb, q_sh, q_st, k_sb, k_sh, k_st, v_sb, v_sh, v_st, o_sb, o_sh, o_st};
   for (int64_t s : strides)
-    if (s % 8) return set_error(SA_E_ALIGN, "sa_prefill: stride %lld is not a multiple of 8 elements", (long long)s);
+    if (s % 8) return set_error(SA_E_ALIGN, "%s: stride %lld is not a multiple of 8 elements", fn, (long long)s);
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o))
-    return set_error(SA_E_ALIGN, "sa_prefill: tensor base pointers must be 16-byte aligned");
+    return set_error(SA_E_ALIGN, "%s: tensor base pointers must be 16-byte aligned", fn);
   if (k_st < 0 || v_st < 0 || k_st > MAX_KV_STRIDE || v_st > MAX_KV_STRIDE)
-    return set_error(SA_E_SHAPE, "sa_prefill: K/V token strides %lld, %lld outside [0, %lld]", (long long)k_st,
+    return set_error(SA_E_SHAPE, "%s: K/V token strides %lld, %lld outside [0, %lld]", fn, (long long)k_st,
                      (long long)v_st, (long long)MAX_KV_STRIDE);
 
   PrefillArgs a;
@@ -1530,26 +1628,90 @@ extern "C" int sa_prefill(int dtype,
   a.mul_R = 0xFFFFFFFFu / (uint32_t)a.R;
   a.mul_hs = 0xFFFFFFFFu / (uint32_t)a.head_splits;
   if (workspace && workspace_bytes < sa_prefill_workspace_bytes())
-    return set_error(SA_E_WORKSPACE, "sa_prefill: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+    return set_error(SA_E_WORKSPACE, "%s: workspace of %lld bytes, need %lld", fn, (long long)workspace_bytes,
                      (long long)sa_prefill_workspace_bytes());
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 3))
-    return set_error(SA_E_ALIGN, "sa_prefill: workspace must be 4-byte aligned");
+    return set_error(SA_E_ALIGN, "%s: workspace must be 4-byte aligned", fn);
   a.counter = static_cast<unsigned int*>(workspace);
 
   const int64_t per_tile = (int64_t)a.R * B * a.head_splits;
   const int64_t n_items = (int64_t)a.ntq * per_tile;
   const int64_t chunk = XCD_CHUNK * per_tile;
   const int64_t item_grid = ceil_div(ceil_div(n_items, chunk), N_XCD) * N_XCD * chunk;
-  if (item_grid > 0x7fffffff) return set_error(SA_E_SHAPE, "sa_prefill: %lld work items is too many", (long long)n_items);
+  if (item_grid > 0x7fffffff) return set_error(SA_E_SHAPE, "%s: %lld work items is too many", fn, (long long)n_items);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == SA_DTYPE_BF16;
   hipError_t err;
-  if (D == 128)
+  a.timeline = timeline;
+  if (timeline) {
+    if (!workspace || hw != 4 || D != 128 || tiled)
+      return set_error(SA_E_SHAPE, "%s: the timeline instruments the persistent four-head kernel (a workspace, "
+                       "four query heads per CSR row, head dim 128, block 64 or 128)", fn);
+    const int64_t grid = std::min<int64_t>(n_items, timeline_grid(bf16));
+    if (timeline_words < grid * TL_WORDS)
+      return set_error(SA_E_WORKSPACE, "%s: timeline of %lld words, need %lld", fn, (long long)timeline_words,
+                       (long long)(grid * TL_WORDS));
+    if (bf16)
+      hipLaunchKernelGGL((prefill_timeline_kernel<true>), dim3(grid), dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL((prefill_timeline_kernel<false>), dim3(grid), dim3(512), 0, s, a);
+    err = hipGetLastError();
+  } else if (D == 128)
     err = bf16 ? launch_d<true, 128>(a, hw, n_items, item_grid, s) : launch_d<false, 128>(a, hw, n_items, item_grid, s);
   else
     err = bf16 ? launch_d<true, 64>(a, hw, n_items, item_grid, s) : launch_d<false, 64>(a, hw, n_items, item_grid, s);
-  if (err != hipSuccess) return set_error((int)err, "sa_prefill: launch failed: %s", hipGetErrorString(err));
+  if (err != hipSuccess) return set_error((int)err, "%s: launch failed: %s", fn, hipGetErrorString(err));
   return 0;
+}
+
+}  // namespace sa
+
+extern "C" int sa_prefill(int dtype,
+                          const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                          const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                          const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                          void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                          const int32_t* pairs, int64_t pairs_stride,
+                          const int32_t* offsets, int64_t offsets_stride,
+                          const int32_t* tile_masks, int64_t tile_masks_stride,
+                          int csr_rows, int nqb,
+                          int B, int Hq, int Hkv, int T_q, int T_k, int D,
+                          int block_size, int q_offset, float sm_scale,
+                          void* workspace, int64_t workspace_bytes,
+                          void* stream) {
+  return sa::prefill_impl("sa_prefill", dtype, q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh, v_st,
+                          o, o_sb, o_sh, o_st, pairs, pairs_stride, offsets, offsets_stride, tile_masks,
+                          tile_masks_stride, csr_rows, nqb, B, Hq, Hkv, T_q, T_k, D, block_size, q_offset,
+                          sm_scale, workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+extern "C" int sa_prefill_timeline(int dtype,
+                                   const void* q, int64_t q_sb, int64_t q_sh, int64_t q_st,
+                                   const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                                   const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                                   void* o, int64_t o_sb, int64_t o_sh, int64_t o_st,
+                                   const int32_t* pairs, int64_t pairs_stride,
+                                   const int32_t* offsets, int64_t offsets_stride,
+                                   int csr_rows, int nqb,
+                                   int B, int Hq, int Hkv, int T_q, int T_k, int D,
+                                   int block_size, int q_offset, float sm_scale,
+                                   void* workspace, int64_t workspace_bytes,
+                                   uint64_t* timeline, int64_t timeline_words,
+                                   void* stream) {
+  sa::clear_error();
+  if (!timeline) return sa::set_error(SA_E_NULL, "sa_prefill_timeline: NULL timeline");
+  return sa::prefill_impl("sa_prefill_timeline", dtype, q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb, v_sh,
+                          v_st, o, o_sb, o_sh, o_st, pairs, pairs_stride, offsets, offsets_stride, nullptr, 0,
+                          csr_rows, nqb, B, Hq, Hkv, T_q, T_k, D, block_size, q_offset, sm_scale, workspace,
+                          workspace_bytes, stream, reinterpret_cast<unsigned long long*>(timeline),
+                          timeline_words);
+}
+
+extern "C" int64_t sa_prefill_timeline_words(int dtype) {
+  sa::clear_error();
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_F16)
+    return sa::set_error(SA_E_DTYPE, "sa_prefill_timeline_words: dtype %d is not bf16 (0) or f16 (1)", dtype);
+  return sa::timeline_grid(dtype == SA_DTYPE_BF16) * sa::TL_WORDS;
 }
 
 extern "C" int64_t sa_prefill_workspace_bytes(void) { return sa::WS_WORDS * (int64_t)sizeof(unsigned int); }

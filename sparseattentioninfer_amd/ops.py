@@ -452,6 +452,87 @@ def prepare_prefill(q, k, v, block_pairs, block_pair_offsets, block_size, *, out
     return PreparedLaunch("sa_prefill", args, (q, k, v, pairs, offsets, sp, so, sm), out)
 
 
+TIMELINE_RECORD_WORDS = 36    # words per workgroup written by sa_prefill_timeline
+TIMELINE_PHASES = ("gap", "setup_and_q_issue", "first_pops", "first_kv_issue", "lookahead_issue", "load_wait",
+                   "barrier", "first_qk", "loop", "last_tile", "epilogue")
+
+
+def prepare_prefill_timeline(q, k, v, block_pairs, block_pair_offsets, block_size, *, out=None) -> PreparedLaunch:
+    """:func:`prepare_prefill` through the instrumented copy of the persistent four-head kernel
+    (``sa_prefill_timeline``; block 64 or 128, four query heads per CSR row, head dim 128).  Each
+    launch writes the same output and a per-workgroup timeline into ``launch.timeline`` (int64,
+    :data:`TIMELINE_RECORD_WORDS` words per workgroup; :func:`summarize_prefill_timeline` reads it).
+    The stamps cost about 100 shader clocks each, so its timing is not the product kernel's."""
+    name = "prepare_prefill_timeline"
+    _check_qkv(q, k, v, name)
+    B, Hq, T_q, D = q.shape
+    Hkv, T_k = k.shape[1], k.shape[2]
+    _require(T_q > 1 and block_size in (64, 128), f"{name}: needs T_q > 1 and block 64/128")
+    pairs = block_pairs.contiguous()
+    offsets = block_pair_offsets.contiguous()
+    _require(pairs.dtype == torch.int32 and offsets.dtype == torch.int32, f"{name}: CSR must be int32")
+    R = pairs.size(0)
+    _require(R in (Hq, Hkv) and offsets.size(1) - 1 == -(-T_q // block_size),
+             f"{name}: CSR rows {R} not Hq or Hkv, or its query blocks do not cover T_q")
+    lib = _lib.load()
+    words = int(lib.sa_prefill_timeline_words(_DTYPES[q.dtype]))
+    _lib.check("sa_prefill_timeline_words", 0 if words > 0 else words)
+    timeline = torch.zeros(words, dtype=torch.int64, device=q.device)
+    if out is None:
+        out = torch.empty(B, Hq, T_q, D, dtype=q.dtype, device=q.device)
+    args = [
+        _DTYPES[q.dtype],
+        q.data_ptr(), q.stride(0), q.stride(1), q.stride(2),
+        k.data_ptr(), k.stride(0), k.stride(1), k.stride(2),
+        v.data_ptr(), v.stride(0), v.stride(1), v.stride(2),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+        pairs.data_ptr(), pairs.stride(0), offsets.data_ptr(), offsets.stride(0),
+        R, offsets.size(1) - 1, B, Hq, Hkv, T_q, T_k, D, block_size, T_k - T_q,
+        1.0 / math.sqrt(D), *_ws_args(_prefill_workspace(q)), timeline.data_ptr(), words, _stream(q)]
+    launch = PreparedLaunch("sa_prefill_timeline", args, (q, k, v, pairs, offsets, timeline), out)
+    launch.timeline = timeline
+    return launch
+
+
+def summarize_prefill_timeline(timeline: torch.Tensor) -> dict:
+    """Summary of one ``sa_prefill_timeline`` launch's records (workgroups that wrote none are
+    skipped): the shader clock (s_memtime against the 100 MHz s_memrealtime), per-item shader
+    clocks of each phase for the first wave of the lower and of the upper 32-row half, loop
+    clocks per step, and the spread of workgroup start and end times."""
+    import numpy as np
+    rec = timeline.detach().cpu().numpy().astype(np.int64).reshape(-1, TIMELINE_RECORD_WORDS)
+    rec = rec[rec[:, 3] > rec[:, 1]]
+    if rec.shape[0] == 0:
+        raise ValueError("summarize_prefill_timeline: no workgroup wrote a record")
+    mt0, rt0, mt1, rt1 = (rec[:, i].astype(np.float64) for i in range(4))
+    halves = rec[:, 4:].reshape(-1, 2, 16) & 0xFFFFFFFF
+    items = halves[:, 0, 12].sum()
+    steps = halves[:, 0, 13].sum()
+    clock = float(np.median((mt1 - mt0) / (rt1 - rt0))) * 0.1       # GHz: s_memrealtime runs at 100 MHz
+    per_item = {}
+    for h, half in enumerate(("lower", "upper")):
+        tot = halves[:, h, :11].sum(axis=0)
+        per_item[half] = {p: round(float(tot[i]) / max(items, 1)) for i, p in enumerate(TIMELINE_PHASES)}
+        per_item[half]["total"] = round(float(tot.sum()) / max(items, 1))
+    end_us = (rt1 - rt0.min()) / 100.0
+    start_us = (rt0 - rt0.min()) / 100.0
+    return {
+        "workgroups": int(rec.shape[0]),
+        "items": int(items),
+        "loop_steps": int(steps),
+        "clock_ghz": round(clock, 3),
+        "steps_per_item": round(float(steps) / max(items, 1), 2),
+        "loop_clocks_per_step": {half: round(float(halves[:, h, 8].sum()) / max(int(halves[:, h, 13].sum()), 1))
+                                 for h, half in enumerate(("lower", "upper"))},
+        "refits": int(halves[:, :, 14].sum()),
+        "clocks_per_item": per_item,
+        "workgroup_start_spread_us": round(float(start_us.max()), 2),
+        "workgroup_end_us": {"min": round(float(end_us.min()), 2), "median": round(float(np.median(end_us)), 2),
+                             "max": round(float(end_us.max()), 2)},
+        "mean_idle_at_end_us": round(float((end_us.max() - end_us).mean()), 2),
+    }
+
+
 def prepare_paged_decode(q, k_pages, v_pages, block_table, kv_lens, sel, sel_off, *,
                          num_splits: int = 1, out=None) -> PreparedLaunch:
     """Validates like :func:`paged_sparse_decode` and binds the launch (workspace included)."""

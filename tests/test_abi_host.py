@@ -94,6 +94,22 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     assert lib.sa_lds_read_rate(1, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
     assert lib.sa_stage_rate(fake, 1024, 10, fake, 1 << 20, None) != 0 and b"needs 65536" in lib.sa_last_error()
     assert lib.sa_stage_rate(fake, 1 << 16, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
+    # the timeline launch instruments only the persistent four-head kernel (workspace, four query heads
+    # per CSR row, head dim 128) and refuses anything else, or a short record buffer, before any launch
+
+    def timeline(D, ws, words, tl=fake, csr_rows=2):
+        return lib.sa_prefill_timeline(0, fake, 8, 8, 8, fake, 8, 8, 8, fake, 8, 8, 8, fake, 8, 8, 8,
+                                       fake, 8, fake, 8, csr_rows, 2, 1, 8, 2, 100, 100, D, 64, 0, 0.1,
+                                       ws, 32 if ws else 0, tl, words, None)
+
+    assert timeline(128, fake, 1 << 20, tl=None) == -6 and b"NULL timeline" in lib.sa_last_error()
+    assert timeline(128, None, 1 << 20) == -2 and b"four-head" in lib.sa_last_error()
+    assert timeline(64, fake, 1 << 20) == -2 and b"four-head" in lib.sa_last_error()
+    assert timeline(128, fake, 1 << 20, csr_rows=8) == -2 and b"four-head" in lib.sa_last_error()
+    assert timeline(128, fake, 35) == -7 and b"timeline of 35 words" in lib.sa_last_error()
+    words = lib.sa_prefill_timeline_words(0)
+    assert words > 0 and words % 36 == 0
+    assert lib.sa_prefill_timeline_words(7) == -1
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

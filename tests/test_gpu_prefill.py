@@ -347,3 +347,32 @@ def test_long_rows_with_unusable_entries(bs, Hq):
     assert torch.equal(out, out_j), "skipped entries changed the result"
     want = oa.block_sparse_attention(q, k, v, pairs, offsets, bs)
     assert_close_bf16(out, want, f"long rows bs={bs} Hq={Hq}")
+
+
+def test_timeline_launch_matches_product_and_counts_the_schedule():
+    """The instrumented persistent kernel (sa_prefill_timeline) writes the product kernel's bits, and
+    its counters hold the schedule: one record per workgroup, every work item once, and one loop step
+    per usable tile after an item's first (its last tile runs outside the loop)."""
+    _say("[prefill] timeline launch")
+    B, Hq, Hkv, T, D, bs = 2, 8, 2, 777, 128, 64
+    bm = bernoulli_block_mask(Hkv, -(-T // bs), -(-T // bs), density=0.3, seed=5)
+    pairs, offsets = (x.to(DEV) for x in block_mask_to_csr(bm))
+    q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=13))
+    want = ops.prepare_prefill(q, k, v, pairs, offsets, bs)()
+    launch = ops.prepare_prefill_timeline(q, k, v, pairs, offsets, bs)
+    got = launch()
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert ops.prefill_workspace_status() == 0
+    s = ops.summarize_prefill_timeline(launch.timeline)
+    ntq = -(-T // 64)
+    n_items = ntq * Hkv * B               # one item per (query tile, CSR row, batch): four heads each
+    counts = (offsets[:, 1:] - offsets[:, :-1]).cpu()   # retained blocks per (row, query block)
+    steps = int(B * (counts - 1).clamp(min=0).sum())
+    assert s["workgroups"] == min(n_items, launch.timeline.numel() // ops.TIMELINE_RECORD_WORDS), s
+    assert s["items"] == n_items, s
+    assert s["loop_steps"] == steps, (s["loop_steps"], steps)
+    assert 0.5 < s["clock_ghz"] < 3.0, s
+    for half in ("lower", "upper"):
+        c = s["clocks_per_item"][half]
+        assert c["total"] > 0 and all(x >= 0 for x in c.values()), c
