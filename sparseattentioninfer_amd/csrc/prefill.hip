@@ -654,15 +654,32 @@ struct Prefill {
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("" ::: "memory");
     elem_t* ob = a.o + b * a.o_sb + it.hq * a.o_sh;
+    constexpr int NR = QT / RPI;  // wave-wide reads (and stores) of the 32 rows
+    // The lane's chunk, opaque to the compiler: the per-row offsets below are then computed here
+    // instead of being hoisted out of the item loop, where they would stay live across the tile
+    // loop (and spill).
+    int lane_e = lane;
+    asm volatile("" : "+v"(lane_e));
+    const int p = lane_e % NCH;
+    auto dst = [&](int row) {
+      return reinterpret_cast<u32x4*>(ob + (int64_t)(it.q_row0 + row) * a.o_st + 8 * (p ^ (row & (NCH - 1))));
+    };
+    // Non-temporal stores: O is not read again here, so it need not displace K/V lines in L2.
+    if (it.q_row0 + QT <= a.Tq) {
+      // Every row exists: all reads are issued before the first store, so the LDS round trips
+      // overlap (a store guarded per lane would keep its read inside the guard, one wait each).
+      u32x4 w[NR];
 #pragma unroll
-    for (int k = 0; k < QT / RPI; ++k) {
-      const int row = RPI * k + lane / NCH;
-      const int p = lane % NCH;
-      const u32x4 w = *reinterpret_cast<const u32x4*>(stage + row * 2 * D + 16 * p);
-      const int qrow = it.q_row0 + row;
-      // Non-temporal: O is not read again here, so it need not displace K/V lines in L2.
-      if (qrow < a.Tq)
-        __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>(ob + (int64_t)qrow * a.o_st + 8 * (p ^ (row & (NCH - 1)))));
+      for (int k = 0; k < NR; ++k) w[k] = *reinterpret_cast<const u32x4*>(stage + (RPI * k + lane_e / NCH) * 2 * D + 16 * p);
+#pragma unroll
+      for (int k = 0; k < NR; ++k) __builtin_nontemporal_store(w[k], dst(RPI * k + lane_e / NCH));
+    } else {
+#pragma unroll
+      for (int k = 0; k < NR; ++k) {
+        const int row = RPI * k + lane_e / NCH;
+        const u32x4 w = *reinterpret_cast<const u32x4*>(stage + row * 2 * D + 16 * p);
+        if (it.q_row0 + row < a.Tq) __builtin_nontemporal_store(w, dst(row));
+      }
     }
   }
 
