@@ -27,6 +27,8 @@
 //    only when a lane's probabilities of one tile sum past 2^16 or overflow; smaller
 //    workgroups raise it when a row max exceeds it by more than 2^8.  Either way the
 //    common case never touches O with VALU;
+//  * the last tile of a four-head item skips the PV half (and the probabilities) of keys
+//    32..63 in a wave whose rows all end before them: the lower half on a diagonal tile;
 //  * O is written back through LDS so that every global store is a 16-byte piece of a
 //    contiguous row;
 //  * with a workspace, one persistent workgroup per CU slot claims work items from an
@@ -1072,11 +1074,12 @@ struct Prefill {
 
     // Probabilities of the tile whose masked scores are Sc, against the current reference:
     // P and this lane's share of the row sum.
-    auto probs = [&](const f32x16 (&Sc)[2], float& ls) {
-      uint32_t pw[2][2][4];
+    auto probs = [&](const f32x16 (&Sc)[2], float& ls, auto halves_tag) {
+      constexpr int NJ = decltype(halves_tag)::value;  // key halves with visible keys (2, or 1: the second is all 0)
+      uint32_t pw[2][2][4] = {};
       ls = 0.f;
 #pragma unroll
-      for (int x = 0; x < 32; x += 2) {
+      for (int x = 0; x < 16 * NJ; x += 2) {
         const int j = x >> 4, rr = x & 15;
         const float p0 = fast_exp2(fmaf(Sc[j][rr], c, neg_m));
         const float p1 = fast_exp2(fmaf(Sc[j][rr + 1], c, neg_m));
@@ -1109,7 +1112,7 @@ struct Prefill {
       m_ref = m_new;
       neg_m = m_ref == -__builtin_inff() ? 0.f : -m_ref;
       ref_ok = !__any(m_ref == -__builtin_inff());
-      probs(Sc, ls);
+      probs(Sc, ls, std::integral_constant<int, 2>{});
     };
 
     // One step on the tile whose scores are in Sc and whose K is in buffer KB, filling Sx
@@ -1197,14 +1200,15 @@ struct Prefill {
       vb_cur = vb_nxt;
     };
     // O^T += V^T P^T of the tile in V buffer cV, nothing else (the last tile).
-    auto block_pv = [&](const char* cV) {
+    auto block_pv = [&](const char* cV, auto halves_tag) {
+      constexpr int NPJ = NP / 2 * decltype(halves_tag)::value;  // MFMAs over the key halves that count
       auto vfr = [&](int i) { return vfrag(cV, f, i / (2 * ND), (i / ND) & 1, i % ND); };
       u32x4 vf[2] = {vfr(0), vfr(1)};
       __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-      for (int i = 0; i < NP; ++i) {
+      for (int i = 0; i < NPJ; ++i) {
         O[i % ND] = E::mfma32(vf[i & 1], P[i / (2 * ND)][(i / ND) & 1], O[i % ND]);
-        if (i + 2 < NP) vf[i & 1] = vfr(i + 2);
+        if (i + 2 < NPJ) vf[i & 1] = vfr(i + 2);
       }
     };
 
@@ -1214,11 +1218,23 @@ struct Prefill {
     auto last_step = [&](f32x16 (&Sc)[2]) {
       const int vb_prev = vb_cur == 0 ? 2 : vb_cur - 1;
       if (lag && pending) block_b(sV + vb_prev * TILE_BYTES);
+      // Keys 32..63 of the last tile lie past every row of this wave (the lower half on a diagonal
+      // tile): their probabilities are 0, so neither they nor their half of the PV product is computed.
+      const int wave_lim = __builtin_amdgcn_readfirstlane(min(it.q_abs_min + QT - 1, a.Tk - 1));
+      const bool lo_only = kt_cur * KT + KT / 2 > wave_lim;
       float ls;
-      probs(Sc, ls);
+      if (lo_only)
+        probs(Sc, ls, std::integral_constant<int, 1>{});
+      else
+        probs(Sc, ls, std::integral_constant<int, 2>{});
       if (!ref_ok || __any(!(ls <= REFIT_SUM))) refit(Sc, ls);
       l_run += ls;
-      if (!lag) block_pv(sV + vb_cur * TILE_BYTES);
+      if (!lag) {
+        if (lo_only)
+          block_pv(sV + vb_cur * TILE_BYTES, std::integral_constant<int, 1>{});
+        else
+          block_pv(sV + vb_cur * TILE_BYTES, std::integral_constant<int, 2>{});
+      }
     };
 
     f32x16 Sn[2];
@@ -1239,7 +1255,7 @@ struct Prefill {
       tl_stamp(TL_LOOP);
       last_step(S);
       // Upper half: PV of the last tile.
-      if (lag) block_pv(sV + vb_cur * TILE_BYTES);
+      if (lag) block_pv(sV + vb_cur * TILE_BYTES, std::integral_constant<int, 2>{});
       vb_first = vb_cur == 2 ? 0 : vb_cur + 1;  // read by neither half in the last step
     }
     tl_stamp(TL_LAST);
