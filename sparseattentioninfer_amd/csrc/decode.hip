@@ -43,11 +43,20 @@ struct DecodeArgs {
   float* part;  // [splits][B][Hq][D + 2] when num_splits > 1
   int B, Hq, Hkv, page, num_splits;
   float scale_log2;
+  // Divisions by launch constants done by multiply-high (fast_div), multipliers from the host:
+  // the workgroup index by num_splits, rows and head_splits, a head by the group size
+  // kv_group = Hq / Hkv, key counts by page, and round indices by the rounds per retained
+  // block rpb = ceil(page / keys per round).
+  int kv_group, rpb;
+  uint32_t mul_splits, mul_rows, mul_hs, mul_group, mul_page, mul_rpb;
 };
 
 constexpr int DEC_WAVES = 4;
 constexpr int DEC_NI = 4;        // 16-byte loads of K (and of V) per lane per round
 constexpr int DEC_CACHE = 512;   // retained blocks of a workgroup staged in LDS (longer lists read HBM)
+
+// Keys one round of a wave covers at head dim D: DEC_NI loads of 64 / (D / 8) key rows.
+constexpr int dec_keys_per_round(int D) { return DEC_NI * (64 / (D / 8)); }
 
 // x as held by the lane that DPP control CTRL selects (quad permutes, row mirrors: within 16 lanes).
 template <int CTRL>
@@ -111,7 +120,8 @@ struct Decode {
   using E = Elem<BF16>;
   static constexpr int LPR = D / 8;        // lanes per key row
   static constexpr int KPI = 64 / LPR;     // key rows per load instruction
-  static constexpr int CH = DEC_NI * KPI;  // keys per round
+  static constexpr int CH = dec_keys_per_round(D);  // keys per round
+  static_assert(CH == DEC_NI * KPI, "keys per round");
 
   // One round of a wave: DEC_NI key rows of K and of V per lane, and the valid key count.
   struct Round {
@@ -125,6 +135,7 @@ struct Decode {
     const int32_t* selp;   // the global list (when not cached)
     const elem_t* safe;    // 16 readable, finite bytes per lane (the query): loads of keys past nk
     int lo, b, kvh, L, rpb, kg, dc;
+    uint32_t mul_rpb;
     uint32_t nb;           // blocks holding keys below L: ids at or past it (or negative) have none
     int n_it;              // rounds of the workgroup; rounds past it are dead (nk = 0)
     bool cached;
@@ -133,7 +144,7 @@ struct Decode {
   // Loads round `it` of the workgroup's list: keys k0 .. k0 + CH - 1 of retained entry it / rpb.
   // Blocks past kv_len or with negative ids, and rounds past the list, have no keys (nk = 0).
   static __device__ __forceinline__ void issue(const DecodeArgs& a, const Ctx& c, int it, Round& R) {
-    const int x = it / c.rpb;
+    const int x = (int)fast_div((uint32_t)it, (uint32_t)c.rpb, c.mul_rpb);  // it >= 0
     const int k0 = (it - x * c.rpb) * CH;
     int lb, pg = 0;
     if (it >= c.n_it) {
@@ -249,13 +260,15 @@ struct Decode {
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    int wid = blockIdx.x;
-    const int s = wid % a.num_splits;
-    wid /= a.num_splits;
-    const int r = wid % a.rows;
-    wid /= a.rows;
-    const int hs = wid % a.head_splits;
-    const int b = wid / a.head_splits;
+    // blockIdx.x = s + num_splits * (r + rows * (hs + head_splits * b))
+    const uint32_t w0 = blockIdx.x;
+    const uint32_t w1 = fast_div(w0, (uint32_t)a.num_splits, a.mul_splits);
+    const int s = (int)(w0 - w1 * (uint32_t)a.num_splits);
+    const uint32_t w2 = fast_div(w1, (uint32_t)a.rows, a.mul_rows);
+    const int r = (int)(w1 - w2 * (uint32_t)a.rows);
+    const uint32_t w3 = fast_div(w2, (uint32_t)a.head_splits, a.mul_hs);
+    const int hs = (int)(w2 - w3 * (uint32_t)a.head_splits);
+    const int b = (int)w3;
     const int h0 = r * a.heads_per_row + hs * NH;  // first query head of this workgroup
 
     Ctx c;
@@ -263,16 +276,22 @@ struct Decode {
     c.kg = lane / LPR;  // key row within a load instruction
     c.b = b;
     c.safe = a.q + b * a.q_sb + h0 * a.q_sh + c.dc * 8;
-    c.kvh = h0 / (a.Hq / a.Hkv);
+    c.kvh = (int)fast_div((uint32_t)h0, (uint32_t)a.kv_group, a.mul_group);
     const int32_t* offp = a.sel_off + b * a.off_sb + r * a.off_sr;
     const int lo_all = offp[0];
     const int cnt = offp[1] - lo_all;
-    c.lo = lo_all + (int)((int64_t)cnt * s / a.num_splits);
-    const int hi = lo_all + (int)((int64_t)cnt * (s + 1) / a.num_splits);
+    int hi = lo_all + cnt;
+    c.lo = lo_all;
+    if (a.num_splits > 1) {  // split s takes entries [cnt * s / S, cnt * (s + 1) / S)
+      c.lo = lo_all + (int)((int64_t)cnt * s / a.num_splits);
+      hi = lo_all + (int)((int64_t)cnt * (s + 1) / a.num_splits);
+    }
     c.selp = a.sel + b * a.sel_sb + r * a.sel_sr;
     c.L = a.kv_lens ? a.kv_lens[b] : a.kv_len;
-    c.rpb = (a.page + CH - 1) / CH;  // rounds per block
-    c.nb = (uint32_t)(((int64_t)max(c.L, 0) + a.page - 1) / a.page);
+    c.rpb = a.rpb;  // rounds per block
+    c.mul_rpb = a.mul_rpb;
+    // blocks holding keys below L: ceil(L / page), L < 2^31 and page <= 128
+    c.nb = fast_div((uint32_t)max(c.L, 0) + (uint32_t)a.page - 1u, (uint32_t)a.page, a.mul_page);
     const int nsel = hi - c.lo;
     c.cached = nsel <= DEC_CACHE;
     c.s_blk = s_blk;
@@ -515,6 +534,14 @@ extern "C" int sa_decode(int dtype,
   a.part = static_cast<float*>(workspace);
   a.B = B; a.Hq = Hq; a.Hkv = Hkv; a.page = page; a.num_splits = num_splits;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
+  a.kv_group = Hq / Hkv;
+  a.rpb = (int)ceil_div(page, dec_keys_per_round(D));
+  a.mul_splits = div_mul((uint32_t)num_splits);
+  a.mul_rows = div_mul((uint32_t)sel_rows);
+  a.mul_hs = div_mul((uint32_t)a.head_splits);
+  a.mul_group = div_mul((uint32_t)a.kv_group);
+  a.mul_page = div_mul((uint32_t)page);
+  a.mul_rpb = div_mul((uint32_t)a.rpb);
 
   const int64_t grid = (int64_t)num_splits * sel_rows * a.head_splits * B;
   if (grid > 0x7fffffff) return set_error(SA_E_SHAPE, "sa_decode: grid too large");

@@ -155,14 +155,6 @@ __device__ __forceinline__ float halves_max(float x) {
   return fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
 }
 
-// floor(n / d) for n < 2^32 and 1 <= d < 2^32, given m = floor((2^32 - 1) / d): m >= (2^32 - d)/d,
-// so the high word of n*m is floor(n/d) or one less, and one compare corrects it.
-__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t d, uint32_t m) {
-  uint32_t q = __umulhi(n, m);
-  q += (n - q * d >= d) ? 1u : 0u;
-  return q;
-}
-
 __device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(const void* p) {
   return (__attribute__((address_space(3))) void*)(p);
 }
@@ -1655,11 +1647,11 @@ static int prefill_impl(const char* fn, int dtype,
   }
   a.head_items = (a.ntq - a.q_split) * a.per_tile;
   a.per_group = std::max(1, a.q_split * a.bhs);
-  a.mul_group = 0xFFFFFFFFu / (uint32_t)a.per_group;
-  a.mul_bhs = 0xFFFFFFFFu / (uint32_t)a.bhs;
-  a.mul_tile = 0xFFFFFFFFu / (uint32_t)a.per_tile;
-  a.mul_R = 0xFFFFFFFFu / (uint32_t)a.R;
-  a.mul_hs = 0xFFFFFFFFu / (uint32_t)a.head_splits;
+  a.mul_group = div_mul((uint32_t)a.per_group);
+  a.mul_bhs = div_mul((uint32_t)a.bhs);
+  a.mul_tile = div_mul((uint32_t)a.per_tile);
+  a.mul_R = div_mul((uint32_t)a.R);
+  a.mul_hs = div_mul((uint32_t)a.head_splits);
   if (workspace && workspace_bytes < sa_prefill_workspace_bytes())
     return set_error(SA_E_WORKSPACE, "%s: workspace of %lld bytes, need %lld", fn, (long long)workspace_bytes,
                      (long long)sa_prefill_workspace_bytes());

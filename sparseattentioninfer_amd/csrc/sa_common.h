@@ -93,4 +93,15 @@ __device__ __forceinline__ uint32_t pack2(elem_t lo, elem_t hi) {
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// floor(n / d) for n < 2^32 and 1 <= d < 2^32, given m = floor((2^32 - 1) / d): m >= (2^32 - d)/d,
+// so the high word of n*m is floor(n/d) or one less, and one compare corrects it.
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, uint32_t d, uint32_t m) {
+  uint32_t q = __umulhi(n, m);
+  q += (n - q * d >= d) ? 1u : 0u;
+  return q;
+}
+
+// The multiplier m of fast_div for divisor d >= 1.
+inline uint32_t div_mul(uint32_t d) { return 0xFFFFFFFFu / d; }
+
 }  // namespace sa
