@@ -104,13 +104,20 @@ __device__ __forceinline__ int32_t load_now(const int32_t* p) {
   return x;
 }
 
+// Block-table entry of logical block lb of sequence b, or NULL where the block has no keys below
+// L or lies past the table's max_blocks columns.
+__device__ __forceinline__ const int32_t* table_slot(const DecodeArgs& a, int b, int lb, int L) {
+  if (lb < 0 || lb >= a.max_blocks || (int64_t)lb * a.page >= L) return nullptr;
+  return a.block_table + b * a.bt_stride + lb;
+}
+
 // Page of logical block lb of sequence b in a paged cache, or -1 where the block has no keys
 // below L, lies past the table's max_blocks columns, or maps outside the pool: such blocks load
 // nothing.  NOW: read the table with load_now (inside the round loop).
 template <bool NOW = false>
 __device__ __forceinline__ int page_of(const DecodeArgs& a, int b, int lb, int L) {
-  if (lb < 0 || lb >= a.max_blocks || (int64_t)lb * a.page >= L) return -1;
-  const int32_t* t = a.block_table + b * a.bt_stride + lb;
+  const int32_t* t = table_slot(a, b, lb, L);
+  if (!t) return -1;
   const int pg = NOW ? load_now(t) : *t;
   return (pg >= 0 && pg < a.num_pages) ? pg : -1;
 }
@@ -141,24 +148,38 @@ struct Decode {
     bool cached;
   };
 
-  // Loads round `it` of the workgroup's list: keys k0 .. k0 + CH - 1 of retained entry it / rpb.
-  // Blocks past kv_len or with negative ids, and rounds past the list, have no keys (nk = 0).
-  static __device__ __forceinline__ void issue(const DecodeArgs& a, const Ctx& c, int it, Round& R) {
+  // Logical block lb and page pg of round `it` (entry it / rpb of the list; lb = -1 for rounds
+  // past the list).  Lists longer than the LDS stage: the entry and its page are read from
+  // global memory with load_now (each waits for every load issued before it).
+  static __device__ __forceinline__ void entry(const DecodeArgs& a, const Ctx& c, int it, int& lb, int& pg) {
     const int x = (int)fast_div((uint32_t)it, (uint32_t)c.rpb, c.mul_rpb);  // it >= 0
-    const int k0 = (it - x * c.rpb) * CH;
-    int lb, pg = 0;
+    pg = 0;
     if (it >= c.n_it) {
       lb = -1;
     } else if (c.cached) {
       lb = c.s_blk[x];
       pg = c.s_pg[x];
-    } else {  // lists longer than the LDS stage: entries read where they are used
+    } else {
       lb = load_now(c.selp + c.lo + x);
       if (a.block_table) {
         pg = page_of<true>(a, c.b, lb, c.L);
         if (pg < 0) lb = -1;
       }
     }
+  }
+
+  static __device__ __forceinline__ void issue(const DecodeArgs& a, const Ctx& c, int it, Round& R) {
+    int lb, pg;
+    entry(a, c, it, lb, pg);
+    issue_at(a, c, it, lb, pg, R);
+  }
+
+  // Loads round `it` of the workgroup's list: keys k0 .. k0 + CH - 1 of logical block lb (page pg).
+  // Blocks past kv_len or with negative ids, and rounds past the list, have no keys (nk = 0).
+  static __device__ __forceinline__ void issue_at(const DecodeArgs& a, const Ctx& c, int it, int lb, int pg,
+                                                  Round& R) {
+    const int x = (int)fast_div((uint32_t)it, (uint32_t)c.rpb, c.mul_rpb);  // it >= 0
+    const int k0 = (it - x * c.rpb) * CH;
     lb = __builtin_amdgcn_readfirstlane(lb);
     pg = __builtin_amdgcn_readfirstlane(pg);
     // one unsigned test for negative ids and ids at or past the last block (no lb * page overflow)
@@ -296,9 +317,42 @@ struct Decode {
     c.cached = nsel <= DEC_CACHE;
     c.s_blk = s_blk;
     c.s_pg = s_pg;
+    const int n_items = nsel * c.rpb;
+    c.n_it = n_items;
+
     // Stage the list (and its pages) once: the round loop then reads LDS, not dependent HBM loads.
-    if (c.cached)
-      for (int x = tid; x < nsel; x += 64 * DEC_WAVES) {
+    // The first pass (one entry per thread) interleaves with the lookup of this wave's first round,
+    // which reads its entry and page directly: each of the two load_now reads also waits for the
+    // staging load issued before it, so the staging costs no round trip of its own and the first
+    // round's K/V loads go out without waiting for the staged list.
+    Round A, B;
+    int it = wave;
+    const bool st1 = c.cached && tid < nsel;
+    int st_lb = -1, st_pg = 0;
+    if (st1) st_lb = c.selp[c.lo + tid];
+    int lb0, pg0;
+    const int x0 = (int)fast_div((uint32_t)it, (uint32_t)c.rpb, c.mul_rpb);
+    lb0 = it < c.n_it ? load_now(c.selp + c.lo + x0) : -1;
+    // The staged entry's table read is issued here and checked after the next load_now, so it
+    // adds no wait of its own.
+    const int32_t* st_t = (st1 && a.block_table) ? table_slot(a, b, st_lb, c.L) : nullptr;
+    if (st_t) st_pg = *st_t;
+    pg0 = 0;
+    if (it < c.n_it && a.block_table) {
+      pg0 = page_of<true>(a, b, lb0, c.L);
+      if (pg0 < 0) lb0 = -1;
+    }
+    if (st1) {
+      if (a.block_table) {
+        st_pg = (st_t && st_pg >= 0 && st_pg < a.num_pages) ? st_pg : -1;
+        if (st_pg < 0) st_lb = -1;
+      }
+      s_blk[tid] = st_lb;
+      s_pg[tid] = st_pg;
+    }
+    issue_at(a, c, it, lb0, pg0, A);
+    if (c.cached)  // entries past the first pass (lists of more than 64 * DEC_WAVES blocks)
+      for (int x = tid + 64 * DEC_WAVES; x < nsel; x += 64 * DEC_WAVES) {
         int lb = c.selp[c.lo + x];
         int pg = 0;
         if (a.block_table) {
@@ -327,16 +381,11 @@ struct Decode {
     __syncthreads();  // staged list visible
 
     // Rounds it = wave, wave + DEC_WAVES, ...: the next round's loads are issued before the
-    // current round is computed (two register sets, alternating).
-    const int n_items = nsel * c.rpb;
-    c.n_it = n_items;
-    // Every issue is unconditional (a round past the end is a dead one), so the loads form one
-    // straight sequence and the wait before a round's compute leaves the next round in flight.
-    Round A, B;
-    int it = wave;
-    // The fences keep each round's loads where they are written, ahead of the previous round's
-    // compute (the compiler would otherwise sink them below it).
-    issue(a, c, it, A);
+    // current round is computed (two register sets, alternating).  Every issue is unconditional
+    // (a round past the end is a dead one), so the loads form one straight sequence and the wait
+    // before a round's compute leaves the next round in flight.  The fences keep each round's
+    // loads where they are written, ahead of the previous round's compute (the compiler would
+    // otherwise sink them below it).
     for (;;) {
       if (it >= n_items) break;
       issue(a, c, it + DEC_WAVES, B);
