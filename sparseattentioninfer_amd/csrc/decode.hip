@@ -270,19 +270,33 @@ struct Decode {
       }
   }
 
-  static __device__ void run(const DecodeArgs& a) {
-    __shared__ float s_m[DEC_WAVES][NH];
-    __shared__ float s_l[DEC_WAVES][NH];
-    __shared__ float s_acc[DEC_WAVES][NH][D];
-    __shared__ int32_t s_blk[DEC_CACHE];
-    __shared__ int32_t s_pg[DEC_CACHE];
+  // UNITS (1 or 2) independent units per workgroup, DEC_WAVES waves each: unit UNITS * blockIdx.x
+  // + h is run by threads 256 h .. 256 h + 255 with LDS of its own; the units share only the
+  // workgroup's barriers.  A unit index at or past n_units (the second half of the last
+  // workgroup) runs no rounds and writes nothing.
+  template <int UNITS>
+  static __device__ void run(const DecodeArgs& a, int n_units) {
+    __shared__ float s_m_[UNITS][DEC_WAVES][NH];
+    __shared__ float s_l_[UNITS][DEC_WAVES][NH];
+    __shared__ float s_acc_[UNITS][DEC_WAVES][NH][D];
+    __shared__ int32_t s_blk_[UNITS][DEC_CACHE];
+    __shared__ int32_t s_pg_[UNITS][DEC_CACHE];
+    const int half = UNITS == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8);
+    auto& s_m = s_m_[half];
+    auto& s_l = s_l_[half];
+    auto& s_acc = s_acc_[half];
+    int32_t* s_blk = s_blk_[half];
+    int32_t* s_pg = s_pg_[half];
 
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x & (64 * DEC_WAVES - 1);
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int unit_raw = UNITS * (int)blockIdx.x + half;
+    const bool idle = unit_raw >= n_units;
+    const int unit = idle ? n_units - 1 : unit_raw;
 
-    // blockIdx.x = s + num_splits * (r + rows * (hs + head_splits * b))
-    const uint32_t w0 = blockIdx.x;
+    // unit = s + num_splits * (r + rows * (hs + head_splits * b))
+    const uint32_t w0 = (uint32_t)unit;
     const uint32_t w1 = fast_div(w0, (uint32_t)a.num_splits, a.mul_splits);
     const int s = (int)(w0 - w1 * (uint32_t)a.num_splits);
     const uint32_t w2 = fast_div(w1, (uint32_t)a.rows, a.mul_rows);
@@ -313,7 +327,7 @@ struct Decode {
     c.mul_rpb = a.mul_rpb;
     // blocks holding keys below L: ceil(L / page), L < 2^31 and page <= 128
     c.nb = fast_div((uint32_t)max(c.L, 0) + (uint32_t)a.page - 1u, (uint32_t)a.page, a.mul_page);
-    const int nsel = hi - c.lo;
+    const int nsel = idle ? 0 : hi - c.lo;
     c.cached = nsel <= DEC_CACHE;
     c.s_blk = s_blk;
     c.s_pg = s_pg;
@@ -436,7 +450,8 @@ struct Decode {
         As += s_acc[w][h][d] * f;
       }
       const int hq = h0 + h;
-      if (a.num_splits == 1) {
+      if (idle) {
+      } else if (a.num_splits == 1) {
         const float out = Ls > 0.f ? As / Ls : 0.f;
         a.o[b * a.o_sb + hq * a.o_sh + d] = E::from_f32(out);
       } else {
@@ -452,9 +467,10 @@ struct Decode {
 };
 
 // At most 256 registers per lane: at least two waves per SIMD.
-template <bool BF16, int D, int NH>
-__global__ __launch_bounds__(64 * DEC_WAVES) __attribute__((amdgpu_waves_per_eu(2))) void decode_kernel(DecodeArgs a) {
-  Decode<BF16, D, NH>::run(a);
+template <bool BF16, int D, int NH, int UNITS>
+__global__ __launch_bounds__(64 * DEC_WAVES * UNITS) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_kernel(DecodeArgs a, int n_units) {
+  Decode<BF16, D, NH>::template run<UNITS>(a, n_units);
 }
 
 // Merges split partials: out = sum_s acc_s 2^(m_s - M) / sum_s l_s 2^(m_s - M).
@@ -502,13 +518,37 @@ __global__ void decode_combine_kernel(const float* part, elem_t* o, int64_t o_sb
   }
 }
 
-template <bool BF16, int D>
-static hipError_t launch_decode_d(const DecodeArgs& a, int nh, int64_t grid, hipStream_t st) {
-  switch (nh) {
-    case 4: hipLaunchKernelGGL((decode_kernel<BF16, D, 4>), dim3(grid), dim3(64 * DEC_WAVES), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<BF16, D, 2>), dim3(grid), dim3(64 * DEC_WAVES), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_kernel<BF16, D, 1>), dim3(grid), dim3(64 * DEC_WAVES), 0, st, a); break;
+static int decode_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+    cached[dev] = n;
   }
+  return cached[dev];
+}
+
+template <bool BF16, int D, int UNITS>
+static void launch_decode_units(const DecodeArgs& a, int nh, int64_t units, hipStream_t st) {
+  const dim3 grid((unsigned)((units + UNITS - 1) / UNITS)), block(64 * DEC_WAVES * UNITS);
+  switch (nh) {
+    case 4: hipLaunchKernelGGL((decode_kernel<BF16, D, 4, UNITS>), grid, block, 0, st, a, (int)units); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<BF16, D, 2, UNITS>), grid, block, 0, st, a, (int)units); break;
+    default: hipLaunchKernelGGL((decode_kernel<BF16, D, 1, UNITS>), grid, block, 0, st, a, (int)units); break;
+  }
+}
+
+// Two units per workgroup once there are at least two per CU: one 8-wave workgroup per CU starts
+// sooner than two 4-wave ones (configs[3]: 41.39-41.48 against 41.65-41.74 us).  Fewer units keep
+// one per workgroup, so every CU gets one.
+template <bool BF16, int D>
+static hipError_t launch_decode_d(const DecodeArgs& a, int nh, int64_t units, hipStream_t st) {
+  if (units >= 2 * (int64_t)decode_cus())
+    launch_decode_units<BF16, D, 2>(a, nh, units, st);
+  else
+    launch_decode_units<BF16, D, 1>(a, nh, units, st);
   return hipGetLastError();
 }
 

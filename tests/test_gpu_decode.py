@@ -51,6 +51,12 @@ DCASES = [
     # more splits than retained blocks (empty splits carry m = -inf, l = 0)
     ("splits16", 2, 8, 2, 128, 64, [9000, 2100], "kv", 16, torch.bfloat16),
     ("splits21_empty", 3, 8, 2, 128, 64, [5000, 700, 64], "kv", 21, torch.bfloat16),
+    # at least two units (sequence, row, split) per CU run two per workgroup: an odd count leaves
+    # the last workgroup's second half without a unit (513 and 3 * 171 units on 256 CUs)
+    ("paired_odd", 513, 4, 1, 128, 64, [(64, 200, 1000, 65, 1)[i % 5] for i in range(513)], "kv", 1,
+     torch.bfloat16),
+    ("paired_odd_splits", 171, 4, 1, 128, 64, [(3000, 64, 700)[i % 3] for i in range(171)], "kv", 3,
+     torch.bfloat16),
 ]
 
 
