@@ -349,15 +349,16 @@ def test_long_rows_with_unusable_entries(bs, Hq):
     assert_close_bf16(out, want, f"long rows bs={bs} Hq={Hq}")
 
 
-def test_timeline_launch_matches_product_and_counts_the_schedule():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+def test_timeline_launch_matches_product_and_counts_the_schedule(dtype):
     """The instrumented persistent kernel (sa_prefill_timeline) writes the product kernel's bits, and
     its counters hold the schedule: one record per workgroup, every work item once, and one loop step
     per usable tile after an item's first (its last tile runs outside the loop)."""
-    _say("[prefill] timeline launch")
+    _say(f"[prefill] timeline launch {dtype}")
     B, Hq, Hkv, T, D, bs = 2, 8, 2, 777, 128, 64
     bm = bernoulli_block_mask(Hkv, -(-T // bs), -(-T // bs), density=0.3, seed=5)
     pairs, offsets = (x.to(DEV) for x in block_mask_to_csr(bm))
-    q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T, T, D, torch.bfloat16, seed=13))
+    q, k, v = (x.to(DEV) for x in _case_inputs(B, Hq, Hkv, T, T, D, dtype, seed=13))
     want = ops.prepare_prefill(q, k, v, pairs, offsets, bs)()
     launch = ops.prepare_prefill_timeline(q, k, v, pairs, offsets, bs)
     got = launch()
