@@ -400,13 +400,22 @@ struct Decode {
     // before a round's compute leaves the next round in flight.  The fences keep each round's
     // loads where they are written, ahead of the previous round's compute (the compiler would
     // otherwise sink them below it).
+    // A wave's last round issues nothing after it: loads still in flight when the loop ends would
+    // be waited for before the merge.
     for (;;) {
       if (it >= n_items) break;
+      if (it + DEC_WAVES >= n_items) {
+        compute(A, qp, a.scale_log2, c.kg, m_run, l_run, acc);
+        break;
+      }
       issue(a, c, it + DEC_WAVES, B);
       asm volatile("" ::: "memory");
       compute(A, qp, a.scale_log2, c.kg, m_run, l_run, acc);
       it += DEC_WAVES;
-      if (it >= n_items) break;
+      if (it + DEC_WAVES >= n_items) {
+        compute(B, qp, a.scale_log2, c.kg, m_run, l_run, acc);
+        break;
+      }
       issue(a, c, it + DEC_WAVES, A);
       asm volatile("" ::: "memory");
       compute(B, qp, a.scale_log2, c.kg, m_run, l_run, acc);
