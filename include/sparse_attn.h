@@ -315,10 +315,11 @@ int sa_stage_rate(const void* src, int64_t src_bytes, int iters, uint32_t* sink,
  * launch, 36 words at timeline[36 * w]: start and end in shader clocks
  * (s_memtime) and in the 100 MHz constant clock (s_memrealtime); then for the
  * first wave of the lower and of the upper 32-row half, 16 words each: the
- * shader clocks spent in the phases of its items (0 gap before an item,
+ * shader clocks spent in the phases of its items (11 from the end of the
+ * previous item to the top of the item loop, 0 from there to the item's setup,
  * 1 setup and Q load issue, 2 first tile-queue pops, 3 first K/V load issue,
  * 4 lookahead issue, 5 load wait, 6 barrier, 7 first S^T, 8 tile loop, 9 last
- * tile, 10 epilogue; 11 unused) and counts (12 items, 13 loop steps, 14 row
+ * tile, 10 epilogue) and counts (12 items, 13 loop steps, 14 row
  * reference refits; 15 the last stamp).  Each stamp costs about 100 shader
  * clocks of its own.  timeline_words >= sa_prefill_timeline_words(dtype), the
  * size for the largest grid on the current device.

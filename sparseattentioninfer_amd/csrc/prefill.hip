@@ -124,7 +124,7 @@ __shared__ int s_row_rank[MAX_ORDERED_ROWS];
 // the record holds TL_WORDS words: start and end in shader clocks and in the 100 MHz constant
 // clock (s_memrealtime), then the 16 words of the lower half and the 16 of the upper half.
 enum : int {
-  TL_GAP = 0,        // end of the previous item (or workgroup start) to this item's setup
+  TL_GAP = 0,        // top of the item loop to this item's setup (metadata reads)
   TL_SETUP_Q = 1,    // item setup and the Q load issue
   TL_POPS = 2,       // tile queue start and the first two pops
   TL_KV = 3,         // direct loads of the first K/V tiles issued
@@ -135,6 +135,7 @@ enum : int {
   TL_LOOP = 8,       // the tile loop (every step but the last tile's)
   TL_LAST = 9,       // the last tile's probabilities and PV
   TL_EPILOGUE = 10,  // normalisation, O staged and stored
+  TL_LOOP_TOP = 11,  // end of the previous item (or workgroup start) to the top of the item loop
   TL_ITEMS = 12,     // counts: items,
   TL_STEPS = 13,     // loop steps,
   TL_REFITS = 14,    // refits of the row reference
@@ -1377,6 +1378,7 @@ struct Prefill {
     }
     __syncthreads();  // publishes the row cache of item 0
     for (int i = 0;; ++i) {
+      tl_stamp(TL_LOOP_TOP);
       // The metadata of item i was published by item i - 1's barriers; the K/V buffers are
       // freed by the barrier in the item's prologue.  Values read from LDS are the same in
       // every lane; readfirstlane keeps them (and the addresses derived from them) in scalar

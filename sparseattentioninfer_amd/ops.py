@@ -453,8 +453,8 @@ def prepare_prefill(q, k, v, block_pairs, block_pair_offsets, block_size, *, out
 
 
 TIMELINE_RECORD_WORDS = 36    # words per workgroup written by sa_prefill_timeline
-TIMELINE_PHASES = ("gap", "setup_and_q_issue", "first_pops", "first_kv_issue", "lookahead_issue", "load_wait",
-                   "barrier", "first_qk", "loop", "last_tile", "epilogue")
+TIMELINE_PHASES = ("loop_top_reads", "setup_and_q_issue", "first_pops", "first_kv_issue", "lookahead_issue",
+                   "load_wait", "barrier", "first_qk", "loop", "last_tile", "epilogue", "after_item")
 
 
 def prepare_prefill_timeline(q, k, v, block_pairs, block_pair_offsets, block_size, *, out=None) -> PreparedLaunch:
@@ -511,7 +511,7 @@ def summarize_prefill_timeline(timeline: torch.Tensor) -> dict:
     clock = float(np.median((mt1 - mt0) / (rt1 - rt0))) * 0.1       # GHz: s_memrealtime runs at 100 MHz
     per_item = {}
     for h, half in enumerate(("lower", "upper")):
-        tot = halves[:, h, :11].sum(axis=0)
+        tot = halves[:, h, :12].sum(axis=0)
         per_item[half] = {p: round(float(tot[i]) / max(items, 1)) for i, p in enumerate(TIMELINE_PHASES)}
         per_item[half]["total"] = round(float(tot.sum()) / max(items, 1))
     end_us = (rt1 - rt0.min()) / 100.0
