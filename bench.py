@@ -384,7 +384,8 @@ def machine_ceilings(dev) -> dict:
     wave) at two and four waves per SIMD, sustained over about 0.1 s, the LDS rates of the
     prefill kernel's two fragment reads (``sa_lds_read_rate``: 8 waves per CU, as the kernel runs)
     and the per-CU rate of its tile staging (``sa_stage_rate``: direct loads of L2-resident 16 KiB
-    tiles, a barrier per tile), in bytes per ns per CU."""
+    tiles, a barrier per tile), in bytes per ns per CU; and the prefill loop's steady-state step in three
+    wave layouts (``sa_step_rate``), in ns per step."""
     import torch
     from sparseattentioninfer_amd import _lib
     lib = _lib.load()
@@ -421,6 +422,22 @@ def machine_ceilings(dev) -> dict:
 
     _, ev = _events_time(launch, 5, 2)
     out["staging_direct_load_bytes_per_ns_per_cu"] = 16384 * iters / (ev / 5) / 1e9
+    # the prefill loop's steady-state step in three wave layouts (sa_step_rate): 32-row waves as shipped,
+    # 16-row and 64-row waves as the alternatives; ns per step, and the step's matrix rate (64 products of
+    # 32,768 FLOP per SIMD and step) as a fraction of the sustained MFMA rate measured above
+    steps = 4000
+    clock = out["mfma_bf16_tflops_2_waves_per_simd"] * 1e12 / (cus * 4 * 1024)   # cycles/s at 1,024 FLOP per SIMD-cycle
+    for layout, key in ((0, "32row_8waves"), (1, "16row_16waves"), (2, "64row_4waves")):
+        sink = torch.empty(int(lib.sa_step_rate_threads(layout)) * cus, dtype=torch.float32, device=dev)
+
+        def launch():
+            _lib.check("sa_step_rate", lib.sa_step_rate(layout, src.data_ptr(), src.numel(), steps, sink.data_ptr(),
+                                                        sink.numel(), stream))
+
+        _, ev = _events_time(launch, 5, 2)
+        ns = ev / 5 / steps * 1e9
+        out[f"prefill_step_ns_{key}"] = ns
+        out[f"prefill_step_frac_of_mfma_rate_{key}"] = 2048 / (ns * clock / 1e9)
     out["note"] = ("measured in this run; the published peaks (2.5 PFLOP/s bf16 at 2.4 GHz) assume a clock the "
                    "boxes do not hold under sustained matrix load")
     return out

@@ -306,6 +306,23 @@ int sa_measure_cus(void);
 int sa_stage_rate(const void* src, int64_t src_bytes, int iters, uint32_t* sink, int64_t sink_len, void* stream);
 
 /*
+ * Measurement aid, no counterpart in the reference: the steady-state step of
+ * the prefill loop (one 64-key tile: 2,048 matrix cycles per SIMD of
+ * v_mfma 32x32x16-equivalents, its exponentials, the K and V fragment reads
+ * from LDS, 32 KiB of direct K/V loads per workgroup from src and one barrier)
+ * in one of three wave layouts, one workgroup per CU, `steps` times:
+ * layout 0 = 8 waves x 32 query rows (the shipped kernel's layout), 1 = 16
+ * waves x 16 rows (v_mfma_f32_16x16x32, four waves per SIMD), 2 = 4 waves x 64
+ * rows (one wave per SIMD, O^T in AGPRs).  src: >= 65536 bytes, 16-byte
+ * aligned, L2-resident.  sink_len >= sa_step_rate_threads(layout) *
+ * sa_measure_cus() floats; the sink values are not meaningful.
+ * sa_step_rate_threads returns the workgroup size of a layout, -1 for others.
+ */
+int sa_step_rate(int layout, const void* src, int64_t src_bytes, int steps, float* sink, int64_t sink_len,
+                 void* stream);
+int sa_step_rate_threads(int layout);
+
+/*
  * Measurement aid, no counterpart in the reference: sa_prefill (block size 64
  * or 128, so no tile masks) through an instrumented copy of the persistent
  * four-head kernel, which also writes a per-workgroup timeline.  Needs what

@@ -98,6 +98,8 @@ SIGNATURES = {
     "sa_lds_read_rate": (_i32, [_i32, _i32, _vp, _i64, _vp]),
     "sa_measure_cus": (_i32, []),
     "sa_stage_rate": (_i32, [_vp, _i64, _i32, _vp, _i64, _vp]),
+    "sa_step_rate": (_i32, [_i32, _vp, _i64, _i32, _vp, _i64, _vp]),
+    "sa_step_rate_threads": (_i32, [_i32]),
     "sa_prefill_timeline": (_i32, [
         _i32,
         _vp, _i64, _i64, _i64,

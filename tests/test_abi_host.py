@@ -94,6 +94,11 @@ def test_argument_errors_are_reported_without_a_gpu(lib):
     assert lib.sa_lds_read_rate(1, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
     assert lib.sa_stage_rate(fake, 1024, 10, fake, 1 << 20, None) != 0 and b"needs 65536" in lib.sa_last_error()
     assert lib.sa_stage_rate(fake, 1 << 16, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
+    assert lib.sa_step_rate(3, fake, 1 << 16, 10, fake, 1 << 20, None) != 0 and b"layout 3" in lib.sa_last_error()
+    assert lib.sa_step_rate(0, fake, 1024, 10, fake, 1 << 20, None) != 0 and b"needs 65536" in lib.sa_last_error()
+    assert lib.sa_step_rate(1, fake, 1 << 16, 0, fake, 1 << 20, None) != 0 and b"steps 0" in lib.sa_last_error()
+    assert lib.sa_step_rate(2, fake, 1 << 16, 10, fake, 1, None) != 0 and b"needs" in lib.sa_last_error()
+    assert [lib.sa_step_rate_threads(k) for k in (0, 1, 2, 3)] == [512, 1024, 256, -1]
     # the timeline launch instruments only the persistent four-head kernel (workspace, four query heads
     # per CSR row, head dim 128) and refuses anything else, or a short record buffer, before any launch
 

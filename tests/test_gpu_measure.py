@@ -1,6 +1,7 @@
 """The measurement aids bench.py reads the kernels against: the HBM streaming-read rate, the dense
-bf16 matrix-core rate and the LDS fragment-read rates, each launched through the C ABI; their
-rates must be physically plausible for an MI355X (the published peaks bound them from above)."""
+bf16 matrix-core rate, the LDS fragment-read rates, the staging rate and the prefill step in three
+wave layouts, each launched through the C ABI; their rates must be physically plausible for an
+MI355X (the published peaks bound them from above)."""
 import sys
 
 import pytest
@@ -54,6 +55,13 @@ def test_ceilings_are_plausible():
     per_cu = 16384 * 2000 / t / 1e9
     assert 5 < per_cu < 400, per_cu             # bytes per ns per CU
     assert (sink == 0x01010101).all()           # the tile landed in LDS
+    for layout in (0, 1, 2):
+        _say(f"[measure] step rate layout {layout}")
+        sink = torch.empty(int(lib.sa_step_rate_threads(layout)) * cus, dtype=torch.float32, device="cuda")
+        t = _time(lambda: _lib.check("sa_step_rate", lib.sa_step_rate(layout, src.data_ptr(), src.numel(), 500,
+                                                                      sink.data_ptr(), sink.numel(), stream)))
+        ns = t / 500 * 1e9
+        assert 850 < ns < 20000, (layout, ns)   # 2,048 matrix cycles per step: over 850 ns at 2.4 GHz
     _say("[measure] stream read")
     n = 1 << 28
     buf = torch.ones(n, dtype=torch.uint8, device="cuda")
