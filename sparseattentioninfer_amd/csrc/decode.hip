@@ -7,8 +7,9 @@
 // softmax with fp32 statistics; a sequence/head with no visible key yields 0.
 //
 // Mapping:
-//  * one workgroup (4 waves) = (sequence b, schedule row r, split s): the NH query
-//    heads that read row r share every K/V load (GQA: one read per KV group);
+//  * one unit (4 waves) = (sequence b, schedule row r, split s): the NH query
+//    heads that read row r share every K/V load (GQA: one read per KV group); a
+//    workgroup runs one unit, or two (8 waves) once there are two units per CU;
 //  * a wave streams whole rounds of a retained block: each lane loads 16-byte
 //    chunks (8 head-dim elements) of K and V, D/8 consecutive lanes cover one key
 //    row, so a load instruction reads 64/(D/8) full rows back to back;
