@@ -1,6 +1,7 @@
 """sa_decode_noalloc (split partials in the library's own per-GPU scratch array) against sa_decode
 with a caller workspace: same kernels, so the same bits, on two calls in a row (the second smaller,
-so it reuses the scratch the first left behind), plus the refusal of sizes past the scratch."""
+so it reuses the scratch the first left behind), and as a step captured in a HIP graph and replayed;
+plus the refusal of sizes past the scratch."""
 import math
 import sys
 
@@ -65,6 +66,44 @@ def test_noalloc_decode_equals_workspace_decode_twice():
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert torch.equal(got, want), f"call {call}: max diff {(got.float() - want.float()).abs().max()}"
+
+
+def test_noalloc_decode_replays_in_a_graph():
+    """The caller the entry point is for: a decode step captured in a HIP graph (split partials in the
+    scratch array, then the combine kernel) gives the workspace decode's bits at every replay, with
+    another sa_decode_noalloc call on other inputs run eagerly between the replays (it overwrites the
+    scratch the replay then fills again)."""
+    lib = _lib.load()
+    B, lens, splits = 6, [9000, 64, 4097, 16384, 700, 3000], 7
+    case = _case(B, 32, 8, 128, 64, lens, seed=61)
+    other = _case(B, 32, 8, 128, 64, lens[::-1], seed=62)
+    need = int(lib.sa_decode_workspace_bytes(B, 32, 128, splits))
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    want = torch.empty_like(case[0])
+    want_other = torch.empty_like(other[0])
+    cur = torch.cuda.current_stream().cuda_stream
+    assert lib.sa_decode(*_args(*case, want, splits), ws.data_ptr(), need, cur) == 0, lib.sa_last_error()
+    assert lib.sa_decode(*_args(*other, want_other, splits), ws.data_ptr(), need, cur) == 0, lib.sa_last_error()
+    got = torch.full_like(case[0], float("nan"))
+    got_other = torch.empty_like(other[0])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):   # warm-up outside the capture (the scratch address is looked up once)
+        assert lib.sa_decode_noalloc(*_args(*case, got, splits), s.cuda_stream) == 0, lib.sa_last_error()
+    torch.cuda.synchronize()
+    _say("[noalloc] capture")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        assert lib.sa_decode_noalloc(*_args(*case, got, splits), s.cuda_stream) == 0, lib.sa_last_error()
+    for rep in range(3):
+        got.fill_(float("nan"))
+        assert lib.sa_decode_noalloc(*_args(*other, got_other, splits), cur) == 0, lib.sa_last_error()
+        torch.cuda.synchronize()
+        assert torch.equal(got_other, want_other), f"eager call before replay {rep}"
+        _say(f"[noalloc] replay {rep}")
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {rep}: max diff {(got.float() - want.float()).abs().max()}"
 
 
 def test_noalloc_refuses_sizes_past_its_scratch():
