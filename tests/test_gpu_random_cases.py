@@ -91,15 +91,18 @@ def run_prefill_case(seed: int):
     return assert_close_bf16(out, want, tag)
 
 
-def decode_case(seed: int) -> dict:
-    """A paged cache, its block table and per-row lists (clean and with skipped entries)."""
-    rng = np.random.default_rng(5000 + seed)
+def decode_case(seed: int, many: bool = False) -> dict:
+    """A paged cache, its block table and per-row lists (clean and with skipped entries).  ``many``:
+    129-257 sequences with shorter caches, so that a launch has at least two units (sequence, row,
+    split) per CU of an MI355X and runs two per workgroup."""
+    rng = np.random.default_rng((7000 if many else 5000) + seed)
     page = int(rng.choice([16, 32, 64, 128]))
     D = int(rng.choice([64, 128]))
-    Hkv = int(rng.integers(1, 5))
+    Hkv = int(rng.integers(2, 5)) if many else int(rng.integers(1, 5))
     Hq = Hkv * int(rng.choice([1, 2, 4, 8]))
-    B = int(rng.integers(1, 7))
-    lens = [int(rng.choice([0, 1, int(rng.integers(2, 6000))], p=[0.05, 0.05, 0.9])) for _ in range(B)]
+    B = int(rng.choice([129, 200, 257])) if many else int(rng.integers(1, 7))
+    top = 1500 if many else 6000
+    lens = [int(rng.choice([0, 1, int(rng.integers(2, top))], p=[0.05, 0.05, 0.9])) for _ in range(B)]
     nblk = [-(-L // page) for L in lens]
     max_blocks = max(1, max(nblk)) + int(rng.integers(0, 3))
     P = sum(nblk) + 3
@@ -136,8 +139,8 @@ def _pack(rows, B, R):
     return sel, off
 
 
-def run_decode_case(seed: int):
-    c = decode_case(seed)
+def run_decode_case(seed: int, many: bool = False):
+    c = decode_case(seed, many)
     tag = (f"seed {seed}: B={c['B']} Hq={c['Hq']} Hkv={c['Hkv']} rows={c['R']} D={c['D']} page={c['page']} "
            f"splits={c['splits']} lens={c['lens']} {str(c['dtype'])[6:]}")
     _say(f"[random decode] {tag}")
@@ -165,6 +168,16 @@ def test_random_prefill_case(seed):
 @pytest.mark.parametrize("seed", range(24))
 def test_random_decode_case(seed):
     run_decode_case(seed)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_decode_case_two_units_per_workgroup(seed):
+    c = decode_case(seed, many=True)
+    hpr = c["Hq"] // c["R"]
+    nh = 4 if hpr % 4 == 0 else 2 if hpr % 2 == 0 else 1
+    units = c["B"] * c["R"] * (hpr // nh) * c["splits"]
+    assert units >= 2 * 256, units   # two per CU of the 256 an MI355X has
+    run_decode_case(seed, many=True)
 
 
 def backend_case(seed: int):
